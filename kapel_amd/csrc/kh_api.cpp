@@ -1,0 +1,498 @@
+// The C ABI of libkapel_hip: argument checks, the choice of mode, the
+// workspace, and the plan of launches.
+//
+// Checks follow QuantizedMatmul::infer (kapel-ops/src/matmul.rs:105-150) and
+// the launch's refusals (kapel-cuda/src/device.rs:673-718); the choice of
+// byte activations follows Run<QuantizedMatmul> for Cpu
+// (kapel-cpu/src/matmul.rs:286-301) and bytes::layout (bytes.rs:51-77).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+#include "kh_internal.h"
+
+using namespace kh;
+
+namespace {
+
+uint64_t div_up(uint64_t a, uint64_t b) { return (a + b - 1) / b; }
+uint64_t align_up(uint64_t a, uint64_t b) { return div_up(a, b) * b; }
+
+// Formats the MFMA product reads; the others take the generic kernel.
+bool mfma_format(uint32_t fmt, uint32_t group) {
+    switch (fmt) {
+    case KH_Q8_0: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1:
+    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K:
+        return true;
+    case KH_INT8: case KH_INT4:
+        return group == 32 || group == 64 || group == 128 || group == 256;
+    default:
+        return false;
+    }
+}
+
+// bytes.rs:51-77: the formats read with activations in bytes.
+bool byte_format(uint32_t fmt, uint32_t group) {
+    switch (fmt) {
+    case KH_Q8_0: case KH_Q4_0: case KH_Q4K: case KH_Q5K: case KH_Q6K:
+        return true;
+    case KH_INT8: case KH_INT4:
+        return group == 32 || group == 64 || group == 128;
+    default:
+        return false;
+    }
+}
+
+int groups_per_step(uint32_t fmt) {
+    return (fmt == KH_Q6K || fmt == KH_Q2K || fmt == KH_Q3K) ? 4 : 2;
+}
+
+// Activation rows one launch takes: the slot groups (row, group) of a step
+// fit in MAX_MFMAS MFMAs.
+int rows_per_launch(uint32_t fmt, int planes) {
+    int slot_groups = MAX_MFMAS * slot_groups_per_mfma(planes);
+    return slot_groups / groups_per_step(fmt);
+}
+
+bool float_kind(uint32_t kind) { return kind == KH_F32 || kind == KH_BF16 || kind == KH_F16; }
+uint64_t kind_bytes(uint32_t kind) { return kind == KH_F32 ? 4 : 2; }
+
+// The split of K into segments for one launch: a function of the shapes only
+// (tiles of 16 rows, steps of 64 elements), so the sums are the same on any
+// device.  Enough workgroups to give each of the 256 CUs several, segments of
+// at least 4 steps, whole super-blocks for the 256-element formats.
+struct Split {
+    int segs, seg_steps;
+    size_t lds;
+};
+
+size_t lds_bytes(int rows, int planes, int seg_steps) {
+    size_t span = (size_t)seg_steps * 64;
+    return 16 + (size_t)rows * planes * (span + 16) + (size_t)rows * (span / 32) * 2 * 4 +
+           (size_t)rows * (span / 16) * 4;
+}
+
+Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
+    uint64_t wgs = div_up(tiles, 4);
+    int quantum = (steps % 4 == 0) ? 4 : 1;
+    int want = (int)std::min<uint64_t>(MAX_SEGS, std::max<uint64_t>(1, div_up(1024, wgs)));
+    int seg_steps = (int)align_up(std::max<int>(4, (int)div_up(steps, want)), quantum);
+    seg_steps = std::min(seg_steps, (int)align_up(steps, quantum));
+    while (seg_steps > quantum && lds_bytes(rows, planes, seg_steps) > (size_t)MAX_LDS)
+        seg_steps -= quantum;
+    int segs = (int)div_up(steps, seg_steps);
+    while (segs > MAX_SEGS) {
+        seg_steps += quantum;
+        segs = (int)div_up(steps, seg_steps);
+    }
+    (void)fmt;
+    return Split{segs, seg_steps, lds_bytes(rows, planes, seg_steps)};
+}
+
+// The workspace: the prepared activations, then the partial sums and the
+// counters of the segment split.
+struct Layout {
+    uint64_t kpad;
+    uint64_t planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off;
+    uint64_t partials_off, counters_off, total;
+};
+
+Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats, uint64_t max_wgs) {
+    Layout l{};
+    l.kpad = align_up(std::max<uint64_t>(k, 64), 64);
+    uint64_t at = 0;
+    l.planes_off = at;
+    at = align_up(at + rows * planes * l.kpad, 256);
+    l.xscale_off = at;
+    at = align_up(at + rows * (k / 32) * 4, 256);
+    l.xsum32_off = at;
+    at = align_up(at + rows * (k / 32) * 4, 256);
+    l.xsum16_off = at;
+    at = align_up(at + rows * (k / 16) * 4, 256);
+    l.xsumi16_off = at;
+    at = align_up(at + rows * (k / 16) * 4, 256);
+    l.partials_off = at;
+    // Partial sums of the largest launch: segments x rows x columns.
+    at = align_up(at + partial_floats * 4, 256);
+    l.counters_off = at;
+    at = align_up(at + (max_wgs + 1) * 4, 256);
+    l.total = at;
+    return l;
+}
+
+struct Checked {
+    uint64_t width = 0, max_wgs = 0, partial_floats = 0;
+    bool bytes = false;
+};
+
+// One launch of the MFMA product: weights `members` (one format), rows
+// r0 .. r0 + rows of the activations.
+struct Launch {
+    std::vector<uint32_t> members;
+    int tiles;
+    uint64_t r0;
+    int rows;
+    Split split;
+};
+
+// Every launch of a product, in order: the weights of a format and group,
+// MAX_WEIGHTS at a time, by chunks of activation rows.
+template <class Fn>
+void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, int planes,
+                 Fn fn) {
+    std::vector<bool> done(count, false);
+    for (uint32_t i = 0; i < count; i++) {
+        if (done[i]) continue;
+        const kh_weight &w = weights[i];
+        if (!mfma_format(w.format, w.group)) {
+            done[i] = true;
+            continue;
+        }
+        Launch L;
+        for (uint32_t j = i; j < count && (int)L.members.size() < MAX_WEIGHTS; j++)
+            if (!done[j] && weights[j].format == w.format && weights[j].group == w.group) {
+                L.members.push_back(j);
+                done[j] = true;
+            }
+        L.tiles = 0;
+        for (uint32_t m : L.members) L.tiles += (int)div_up(weights[m].n, 16);
+        if (L.tiles == 0) continue;
+        int steps = (int)div_up(k, 64);
+        int chunk = rows_per_launch(w.format, planes);
+        for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
+            L.r0 = r0;
+            L.rows = (int)std::min<uint64_t>(chunk, rows - r0);
+            L.split = split_k((uint64_t)L.tiles, steps, L.rows, planes, w.format);
+            fn(L);
+        }
+    }
+}
+
+int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, uint32_t flags,
+          Checked &c) {
+    if (count == 0) return KH_ERR_ARITY;
+    if (!weights) return KH_ERR_NULL;
+    if (k > (1ull << 30) || rows > (1ull << 31)) return KH_ERR_OVERFLOW;
+    bool all_bytes = true;
+    uint64_t tiles = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        const kh_weight &w = weights[i];
+        uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+        if (len == 0) return KH_ERR_DTYPE;
+        if (k % len) return KH_ERR_MISALIGNED;
+        if (w.n > (1ull << 31)) return KH_ERR_OVERFLOW;
+        if (w.bytes != w.n * (k / len) * size) return KH_ERR_SHAPE;
+        if (w.n && k && !w.data) return KH_ERR_NULL;
+        uint64_t sum = c.width + w.n;
+        if (sum < c.width) return KH_ERR_OVERFLOW;
+        c.width = sum;
+        all_bytes = all_bytes && byte_format(w.format, w.group);
+        tiles += div_up(w.n, 16);
+    }
+    if (c.width > (1ull << 31)) return KH_ERR_OVERFLOW;
+    c.bytes = (flags & KH_BYTE_ACTIVATIONS) && all_bytes;
+    c.max_wgs = div_up(tiles, 4) + count;
+    if (k > 0 && rows > 0)
+        each_launch(weights, count, k, rows, c.bytes ? 1 : 3, [&](const Launch &L) {
+            if (L.split.segs > 1)
+                c.partial_floats = std::max<uint64_t>(
+                    c.partial_floats, (uint64_t)L.split.segs * L.rows * L.tiles * 16);
+        });
+    return KH_OK;
+}
+
+hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
+                           const void *x, uint64_t rows, uint32_t out_kind, void *out,
+                           const Checked &c, uint8_t *ws, const Layout &l, bool reuse,
+                           hipStream_t s) {
+    int planes = c.bytes ? 1 : 3;
+    hipError_t err;
+    // The activations, once for all weights.
+    bool any_mfma = false;
+    for (uint32_t i = 0; i < count; i++) any_mfma |= mfma_format(weights[i].format, weights[i].group);
+    if (any_mfma && !reuse) {
+        PrepArgs p{};
+        p.x_kind = x_kind;
+        p.x = x;
+        p.rows = rows;
+        p.k = k;
+        p.kpad = l.kpad;
+        p.planes = planes;
+        p.planes_out = reinterpret_cast<int8_t *>(ws + l.planes_off);
+        p.xscale = reinterpret_cast<float *>(ws + l.xscale_off);
+        p.xsum32 = reinterpret_cast<float *>(ws + l.xsum32_off);
+        p.xsum16 = reinterpret_cast<float *>(ws + l.xsum16_off);
+        p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
+        if ((err = launch_prep(p, s)) != hipSuccess) return err;
+    }
+    // Column of each weight.
+    std::vector<uint64_t> col0(count);
+    uint64_t col = 0;
+    for (uint32_t i = 0; i < count; i++) {
+        col0[i] = col;
+        col += weights[i].n;
+    }
+    for (uint32_t i = 0; i < count; i++) {
+        const kh_weight &w = weights[i];
+        if (mfma_format(w.format, w.group) || w.n == 0) continue;
+        GenericArgs g{};
+        g.format = w.format;
+        g.group = w.group;
+        g.w = static_cast<const uint8_t *>(w.data);
+        g.n = w.n;
+        g.row_bytes = w.bytes / w.n;
+        g.k = k;
+        g.rows = rows;
+        g.x_kind = x_kind;
+        g.x = x;
+        g.out_kind = out_kind;
+        g.out = out;
+        g.col0 = col0[i];
+        g.out_stride = c.width;
+        if ((err = launch_generic(g, s)) != hipSuccess) return err;
+    }
+    err = hipSuccess;
+    each_launch(weights, count, k, rows, planes, [&](const Launch &L) {
+        if (err != hipSuccess) return;
+        const kh_weight &w = weights[L.members[0]];
+        QmvArgs a{};
+        a.count = (int)L.members.size();
+        int tiles = 0;
+        for (int m = 0; m < a.count; m++) {
+            const kh_weight &wm = weights[L.members[m]];
+            a.w[m] = static_cast<const uint8_t *>(wm.data);
+            a.n[m] = wm.n;
+            a.col0[m] = col0[L.members[m]];
+            a.tile0[m] = tiles;
+            tiles += (int)div_up(wm.n, 16);
+        }
+        uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+        a.row_bytes = k / len * size;
+        a.k = (int)k;
+        a.steps = (int)div_up(k, 64);
+        a.kpad = l.kpad;
+        a.out_kind = out_kind;
+        a.width = c.width;
+        a.out_stride = c.width;
+        a.partials = reinterpret_cast<float *>(ws + l.partials_off);
+        a.pwidth = (uint64_t)tiles * 16;
+        a.counters = reinterpret_cast<int *>(ws + l.counters_off);
+        uint64_t r0 = L.r0;
+        a.rows = L.rows;
+        a.segs = L.split.segs;
+        a.seg_steps = L.split.seg_steps;
+        a.planes = reinterpret_cast<const int8_t *>(ws + l.planes_off) + r0 * planes * l.kpad;
+        a.xscale = reinterpret_cast<const float *>(ws + l.xscale_off) + r0 * (k / 32);
+        a.xsum32 = reinterpret_cast<const float *>(ws + l.xsum32_off) + r0 * (k / 32);
+        a.xsum16 = reinterpret_cast<const float *>(ws + l.xsum16_off) + r0 * (k / 16);
+        a.xsumi16 = reinterpret_cast<const int32_t *>(ws + l.xsumi16_off) + r0 * (k / 16);
+        a.out = static_cast<uint8_t *>(out) + r0 * c.width * kind_bytes(out_kind);
+        dim3 grid((unsigned)div_up(tiles, 4), (unsigned)L.split.segs);
+        err = launch_qmv(w.format, w.group, planes, a, grid, L.split.lds, s);
+    });
+    return hipSuccess;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *kh_version(void) { return "kapel_hip 0.1 gfx950"; }
+
+const char *kh_error_string(int status) {
+    switch (status) {
+    case KH_OK: return "ok";
+    case KH_ERR_ARITY: return "quantized_matmul: expected 2 or more inputs";
+    case KH_ERR_DTYPE: return "quantized_matmul: unsupported format or float type";
+    case KH_ERR_SHAPE: return "quantized_matmul: expected x [..., K] and w [N, K]";
+    case KH_ERR_MISALIGNED: return "quantized_matmul: K is not a whole number of blocks";
+    case KH_ERR_OVERFLOW: return "quantized_matmul: a size overflows the kernels' range";
+    case KH_ERR_WORKSPACE: return "quantized_matmul: workspace missing or too small";
+    case KH_ERR_HIP: return "quantized_matmul: HIP runtime error";
+    case KH_ERR_NULL: return "quantized_matmul: a required pointer is null";
+    default: return "unknown status";
+    }
+}
+
+uint32_t kh_block_len(uint32_t format, uint32_t group) {
+    switch (format) {
+    case KH_INT8: return group;
+    case KH_INT4: return (group % 2 == 0) ? group : 0;
+    case KH_Q8_0: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1: return 32;
+    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: return 256;
+    default: return 0;
+    }
+}
+
+uint32_t kh_block_bytes(uint32_t format, uint32_t group) {
+    switch (format) {
+    case KH_INT8: return group ? 4 + group : 0;
+    case KH_INT4: return (group && group % 2 == 0) ? 4 + group / 2 : 0;
+    case KH_Q8_0: return 34;
+    case KH_Q4_0: return 18;
+    case KH_Q4_1: return 20;
+    case KH_Q5_0: return 22;
+    case KH_Q5_1: return 24;
+    case KH_Q2K: return 84;
+    case KH_Q3K: return 110;
+    case KH_Q4K: return 144;
+    case KH_Q5K: return 176;
+    case KH_Q6K: return 210;
+    default: return 0;
+    }
+}
+
+uint64_t kh_qmatmul_workspace(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows,
+                              uint32_t flags) {
+    Checked c;
+    if (check(weights, count, k, rows, flags, c) != KH_OK) return 0;
+    return layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.max_wgs).total;
+}
+
+int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
+               const void *x, uint64_t rows, uint32_t out_kind, void *out, uint32_t flags,
+               void *workspace, uint64_t workspace_bytes, void *stream) {
+    Checked c;
+    int status = check(weights, count, k, rows, flags, c);
+    if (status != KH_OK) return status;
+    if (!float_kind(x_kind) || !float_kind(out_kind)) return KH_ERR_DTYPE;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (rows == 0 || c.width == 0) return KH_OK;
+    if (!out) return KH_ERR_NULL;
+    if (k == 0) {
+        // A sum over nothing: zeros (conformity.rs:1424-1428).
+        return launch_fill_bytes(static_cast<uint8_t *>(out), rows * c.width * kind_bytes(out_kind), s) ==
+                       hipSuccess
+                   ? KH_OK
+                   : KH_ERR_HIP;
+    }
+    if (!x) return KH_ERR_NULL;
+    Layout l = layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.max_wgs);
+    if (!workspace || workspace_bytes < l.total) return KH_ERR_WORKSPACE;
+    hipError_t err = plan_and_launch(weights, count, k, x_kind, x, rows, out_kind, out, c,
+                                     static_cast<uint8_t *>(workspace), l,
+                                     (flags & KH_REUSE_ACTIVATIONS) != 0, s);
+    return err == hipSuccess ? KH_OK : KH_ERR_HIP;
+}
+
+int kh_quantize_x(uint32_t x_kind, const void *x, uint64_t rows, uint64_t k, int8_t *q,
+                  float *scale, float *sums32, void *stream) {
+    if (!float_kind(x_kind)) return KH_ERR_DTYPE;
+    if (k % 32) return KH_ERR_MISALIGNED;
+    if (rows * k == 0) return KH_OK;
+    if (!x || !q || !scale) return KH_ERR_NULL;
+    PrepArgs p{};
+    p.x_kind = x_kind;
+    p.x = x;
+    p.rows = rows;
+    p.k = k;
+    p.kpad = k;
+    p.planes = 1;
+    p.q_out = q;
+    p.q_scale = scale;
+    p.q_sums = sums32;
+    return launch_prep(p, static_cast<hipStream_t>(stream)) == hipSuccess ? KH_OK : KH_ERR_HIP;
+}
+
+int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t rows,
+                  int32_t *dots, void *workspace, uint64_t workspace_bytes, void *stream) {
+    Checked c;
+    int status = check(weight, 1, k, rows, KH_BYTE_ACTIVATIONS, c);
+    if (status != KH_OK) return status;
+    if (!c.bytes) return KH_ERR_DTYPE;
+    if (rows == 0 || weight->n == 0 || k == 0) return KH_OK;
+    if (!q || !dots) return KH_ERR_NULL;
+    Layout l = layout(rows, k, 1, c.partial_floats, c.max_wgs);
+    if (!workspace || workspace_bytes < l.total) return KH_ERR_WORKSPACE;
+    uint8_t *ws = static_cast<uint8_t *>(workspace);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    PrepArgs p{};
+    p.q_in = q;
+    p.rows = rows;
+    p.k = k;
+    p.kpad = l.kpad;
+    p.planes = 1;
+    p.planes_out = reinterpret_cast<int8_t *>(ws + l.planes_off);
+    p.xscale = reinterpret_cast<float *>(ws + l.xscale_off);
+    p.xsum32 = reinterpret_cast<float *>(ws + l.xsum32_off);
+    p.xsum16 = reinterpret_cast<float *>(ws + l.xsum16_off);
+    p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
+    if (launch_prep(p, s) != hipSuccess) return KH_ERR_HIP;
+    const kh_weight &w = *weight;
+    QmvArgs a{};
+    a.count = 1;
+    a.w[0] = static_cast<const uint8_t *>(w.data);
+    a.n[0] = w.n;
+    a.col0[0] = 0;
+    a.tile0[0] = 0;
+    uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+    a.row_bytes = k / len * size;
+    a.k = (int)k;
+    a.steps = (int)div_up(k, 64);
+    a.kpad = l.kpad;
+    a.width = w.n;
+    a.out_stride = w.n;
+    a.dots = dots;
+    a.signed_offset = w.format == KH_Q6K ? 32 : 0;
+    int tiles = (int)div_up(w.n, 16);
+    int chunk = rows_per_launch(w.format, 1);
+    for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
+        int rc = (int)std::min<uint64_t>(chunk, rows - r0);
+        Split sp = split_k((uint64_t)tiles, a.steps, rc, 1, w.format);
+        a.rows = rc;
+        a.segs = sp.segs;
+        a.seg_steps = sp.seg_steps;
+        a.planes = reinterpret_cast<const int8_t *>(ws + l.planes_off) + r0 * l.kpad;
+        a.xscale = reinterpret_cast<const float *>(ws + l.xscale_off) + r0 * (k / 32);
+        a.xsum32 = reinterpret_cast<const float *>(ws + l.xsum32_off) + r0 * (k / 32);
+        a.xsum16 = reinterpret_cast<const float *>(ws + l.xsum16_off) + r0 * (k / 16);
+        a.xsumi16 = reinterpret_cast<const int32_t *>(ws + l.xsumi16_off) + r0 * (k / 16);
+        a.dots = dots + r0 * w.n * (k / 16);
+        dim3 grid((unsigned)div_up(tiles, 4), (unsigned)sp.segs);
+        if (launch_qmv(w.format, w.group, 1, a, grid, sp.lds, s) != hipSuccess) return KH_ERR_HIP;
+    }
+    return KH_OK;
+}
+
+static int dequant(const kh_weight *weight, uint64_t k, uint64_t first, uint64_t count,
+                   const uint32_t *indices, uint32_t out_kind, void *out, void *stream) {
+    if (!weight) return KH_ERR_NULL;
+    uint32_t len = kh_block_len(weight->format, weight->group);
+    uint32_t size = kh_block_bytes(weight->format, weight->group);
+    if (len == 0) return KH_ERR_DTYPE;
+    if (!float_kind(out_kind)) return KH_ERR_DTYPE;
+    if (k % len) return KH_ERR_MISALIGNED;
+    if (weight->bytes != weight->n * (k / len) * size) return KH_ERR_SHAPE;
+    if (!indices && first + count > weight->n) return KH_ERR_SHAPE;
+    if (count * k == 0) return KH_OK;
+    if (!out || !weight->data) return KH_ERR_NULL;
+    DequantArgs a{};
+    a.format = weight->format;
+    a.group = weight->group;
+    a.w = static_cast<const uint8_t *>(weight->data);
+    a.n = weight->n;
+    a.row_bytes = k / len * size;
+    a.k = k;
+    a.first = first;
+    a.count = count;
+    a.indices = indices;
+    a.out_kind = out_kind;
+    a.out = out;
+    return launch_dequantize(a, static_cast<hipStream_t>(stream)) == hipSuccess ? KH_OK : KH_ERR_HIP;
+}
+
+int kh_dequantize(const kh_weight *weight, uint64_t k, uint64_t first, uint64_t count,
+                  uint32_t out_kind, void *out, void *stream) {
+    return dequant(weight, k, first, count, nullptr, out_kind, out, stream);
+}
+
+int kh_dequantize_rows(const kh_weight *weight, uint64_t k, const uint32_t *indices, uint64_t count,
+                       uint32_t out_kind, void *out, void *stream) {
+    if (count && !indices) return KH_ERR_NULL;
+    return dequant(weight, k, 0, count, indices, out_kind, out, stream);
+}
+
+}  // extern "C"

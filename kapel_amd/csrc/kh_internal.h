@@ -1,0 +1,96 @@
+// Internal arguments of the kernels of libkapel_hip (host and device).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/kapel_hip.h"
+
+namespace kh {
+
+// Weights per launch of the product (stacked matrices of one format).
+constexpr int MAX_WEIGHTS = 8;
+// MFMAs per step at most: 8 x 4 slot groups with f32 activations, 8 x 16
+// with byte activations (a slot group is one activation row and one group
+// of weights of a step).
+constexpr int MAX_MFMAS = 8;
+// Slot groups of one MFMA: 4 with f32 activations (four rows of A each: the
+// three planes and a zero row), 16 with byte activations (one row each).
+constexpr int slot_groups_per_mfma(int planes) { return planes == 3 ? 4 : 16; }
+// Segments of K at most.
+constexpr int MAX_SEGS = 64;
+// LDS of one workgroup of the product at most.
+constexpr int MAX_LDS = 64 * 1024;
+
+struct PrepArgs {
+    uint32_t x_kind;
+    const void *x;        // [rows, k] floats, or NULL with q_in
+    const int8_t *q_in;   // [rows, k] bytes already quantized (block dots)
+    uint64_t rows, k, kpad;
+    int planes;           // 1: bytes (CPU rule), 3: f32 activations
+    int8_t *planes_out;   // [rows, planes, kpad] or NULL
+    float *xscale;        // [rows, k/32] or NULL
+    float *xsum32;        // [rows, k/32] or NULL
+    float *xsum16;        // [rows, k/16] or NULL
+    int32_t *xsumi16;     // [rows, k/16] or NULL
+    int8_t *q_out;        // [rows, k] or NULL (kh_quantize_x)
+    float *q_scale;       // [rows, k/32] or NULL
+    float *q_sums;        // [rows, k/32] or NULL
+};
+
+struct QmvArgs {
+    // Weights of one format, rows stacked in tiles of 16 (a tile never spans
+    // two weights).
+    int count;
+    const uint8_t *w[MAX_WEIGHTS];
+    uint64_t n[MAX_WEIGHTS];
+    uint64_t col0[MAX_WEIGHTS];   // first output column of each weight
+    int tile0[MAX_WEIGHTS];       // first tile of each weight in this launch
+    uint64_t row_bytes;
+    int k, steps, seg_steps, segs;
+    int rows;                     // activation rows of this launch
+    // Prepared activations of these rows.
+    const int8_t *planes;
+    uint64_t kpad;
+    const float *xscale, *xsum32, *xsum16;
+    const int32_t *xsumi16;
+    // Output [rows, width] with row stride out_stride (elements).
+    uint32_t out_kind;
+    void *out;
+    uint64_t width, out_stride;
+    float *partials;              // [segs, rows, pwidth]: pwidth = 16 x tiles
+    uint64_t pwidth;
+    int *counters;                // [gridDim.x], zero between launches
+    // Block dots instead of the product (kh_block_dots).
+    int32_t *dots;
+    int signed_offset;
+};
+
+struct GenericArgs {
+    uint32_t format, group;
+    const uint8_t *w;
+    uint64_t n, row_bytes, k, rows;
+    uint32_t x_kind;
+    const void *x;
+    uint32_t out_kind;
+    void *out;
+    uint64_t col0, out_stride;
+};
+
+struct DequantArgs {
+    uint32_t format, group;
+    const uint8_t *w;
+    uint64_t n, row_bytes, k, first, count;
+    const uint32_t *indices;
+    uint32_t out_kind;
+    void *out;
+};
+
+hipError_t launch_prep(const PrepArgs &a, hipStream_t s);
+hipError_t launch_fill(uint32_t *p, uint64_t words, hipStream_t s);
+hipError_t launch_fill_bytes(uint8_t *p, uint64_t bytes, hipStream_t s);
+hipError_t launch_qmv(uint32_t fmt, uint32_t group, int planes, const QmvArgs &a, dim3 grid,
+                      size_t lds, hipStream_t s);
+hipError_t launch_generic(const GenericArgs &a, hipStream_t s);
+hipError_t launch_dequantize(const DequantArgs &a, hipStream_t s);
+
+}  // namespace kh

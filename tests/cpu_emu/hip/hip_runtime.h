@@ -1,0 +1,251 @@
+// CPU emulation of the HIP device features libkapel_hip's kernels use, for a
+// host build of the unchanged kernel sources (test infrastructure only).
+//
+// A launch runs its workgroups one after the other; each workgroup is
+// blockDim.x host threads (one per lane), with a barrier for __syncthreads
+// and one per wave of 64 for the wave-wide operations (__shfl_xor and the
+// MFMA), which exchange their operands through per-wave slots.  Built with
+// AddressSanitizer, every global and LDS access of the kernels is bounds
+// checked on the host.
+#pragma once
+#include <barrier>
+#include <condition_variable>
+#include <functional>
+#include <mutex>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#define __global__
+#define __device__
+#define __host__
+#define __forceinline__ inline
+#define __launch_bounds__(...)
+#define __shared__
+#define __align__(n) __attribute__((aligned(n)))
+#define __HIP_MEMORY_SCOPE_AGENT 0
+
+struct dim3 {
+    unsigned x, y, z;
+    constexpr dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
+};
+typedef int hipError_t;
+enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
+typedef struct ihipStream_t *hipStream_t;
+struct int2 {
+    int x, y;
+};
+struct uint2 {
+    unsigned x, y;
+};
+
+namespace emu {
+
+constexpr size_t LDS_BYTES = 160 * 1024;
+
+struct Lane {
+    dim3 tid, bid;
+};
+inline thread_local Lane self;
+
+struct Block {
+    std::barrier<> *all = nullptr;
+    std::barrier<> *wave[16] = {};
+    uint64_t slots[16][64][4];  // per wave, per lane: up to 32 bytes
+    unsigned threads = 0;
+};
+inline Block block;
+
+inline int lane_id() { return (int)(self.tid.x & 63); }
+inline int wave_id() { return (int)(self.tid.x >> 6); }
+inline void wave_sync() { block.wave[wave_id()]->arrive_and_wait(); }
+
+template <class T>
+T shfl_xor(T v, int mask, int width = 64) {
+    static_assert(sizeof(T) <= 8, "shuffled values fit a slot");
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &v, sizeof(T));
+    wave_sync();
+    int src = l ^ mask;
+    if ((src / width) != (l / width)) src = l;
+    T out;
+    std::memcpy(&out, &block.slots[w][src][0], sizeof(T));
+    wave_sync();
+    return out;
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// v_mfma_i32_16x16x64_i8: D[i][j] = C[i][j] + sum_k A[i][k] B[k][j], i, j <
+// 16, k < 64.  Lane l supplies A[l % 16][16 (l / 16) + b] and
+// B[16 (l / 16) + b][l % 16] as bytes b = 0..15 of its 16-byte operand, and
+// receives D[4 (l / 16) + v][l % 16], v = 0..3.
+inline v4i mfma_i8(v4i a, v4i b, v4i c, int, int, int) {
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &a, 16);
+    std::memcpy(&block.slots[w][l][2], &b, 16);
+    wave_sync();
+    v4i d = c;
+    int j = l % 16;
+    for (int v = 0; v < 4; v++) {
+        int i = 4 * (l / 16) + v;
+        int sum = 0;
+        for (int k = 0; k < 64; k++) {
+            int g = k / 16, byte = k % 16;
+            const int8_t *ai = reinterpret_cast<const int8_t *>(&block.slots[w][16 * g + i][0]);
+            const int8_t *bj = reinterpret_cast<const int8_t *>(&block.slots[w][16 * g + j][2]);
+            sum += (int)ai[byte] * (int)bj[byte];
+        }
+        d[v] += sum;
+    }
+    wave_sync();
+    return d;
+}
+
+// v_perm_b32: byte s of the result is byte sel[s] of {hi:lo} (0..3 of lo,
+// 4..7 of hi); selectors above 7 are not used by the kernels.
+inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+    uint64_t both = ((uint64_t)hi << 32) | lo;
+    uint32_t out = 0;
+    for (int s = 0; s < 4; s++) {
+        uint32_t k = (sel >> (8 * s)) & 0xff;
+        if (k > 7) std::abort();
+        out |= (uint32_t)((both >> (8 * k)) & 0xff) << (8 * s);
+    }
+    return out;
+}
+
+template <class T>
+T atomic_load(const T *p) {
+    T v;
+    __atomic_load(p, &v, __ATOMIC_SEQ_CST);
+    return v;
+}
+
+template <class K, class... A>
+void launch(K kernel, dim3 grid, dim3 threads, size_t lds, A... args);
+
+}  // namespace emu
+
+namespace kh {
+alignas(16) inline uint8_t lds[emu::LDS_BYTES];
+}
+
+#define threadIdx (emu::self.tid)
+#define blockIdx (emu::self.bid)
+#define __syncthreads() (emu::block.all->arrive_and_wait())
+#define __threadfence() __atomic_thread_fence(__ATOMIC_SEQ_CST)
+#define __shfl_xor(v, m, ...) emu::shfl_xor((v), (m) __VA_OPT__(, ) __VA_ARGS__)
+#define __builtin_amdgcn_mfma_i32_16x16x64_i8(...) emu::mfma_i8(__VA_ARGS__)
+#define __builtin_amdgcn_perm(hi, lo, s) emu::perm((hi), (lo), (s))
+#define __hip_atomic_fetch_add(p, v, order, scope) __atomic_fetch_add((p), (v), __ATOMIC_SEQ_CST)
+#define __hip_atomic_load(p, order, scope) emu::atomic_load(p)
+#define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)
+#define hipLaunchKernelGGL(kernel, grid, threads, lds, stream, ...) \
+    emu::launch(kernel, dim3(grid), dim3(threads), (size_t)(lds), __VA_ARGS__)
+
+inline hipError_t hipGetLastError() { return hipSuccess; }
+
+inline float __uint_as_float(uint32_t u) {
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+inline uint32_t __float_as_uint(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+inline int min(int a, int b) { return a < b ? a : b; }
+inline int max(int a, int b) { return a > b ? a : b; }
+using std::isfinite;
+
+namespace emu {
+
+// Lane threads, created once and reused by every launch.
+struct Pool {
+    std::vector<std::thread> workers;
+    std::mutex m;
+    std::condition_variable wake, idle;
+    uint64_t generation = 0;
+    unsigned active = 0, finished = 0;
+    std::function<void(unsigned)> job;
+
+    void ensure(unsigned n) {
+        while (workers.size() < n) {
+            unsigned t = (unsigned)workers.size();
+            workers.emplace_back([this, t] {
+                uint64_t seen = 0;
+                for (;;) {
+                    std::function<void(unsigned)> fn;
+                    {
+                        std::unique_lock<std::mutex> lock(m);
+                        wake.wait(lock, [&] { return generation != seen; });
+                        seen = generation;
+                        if (t >= active) continue;
+                        fn = job;
+                    }
+                    fn(t);
+                    std::lock_guard<std::mutex> lock(m);
+                    if (++finished == active) idle.notify_all();
+                }
+            });
+            workers.back().detach();
+        }
+    }
+
+    void run(unsigned n, std::function<void(unsigned)> fn) {
+        ensure(n);
+        std::unique_lock<std::mutex> lock(m);
+        job = std::move(fn);
+        active = n;
+        finished = 0;
+        generation++;
+        wake.notify_all();
+        idle.wait(lock, [&] { return finished == active; });
+    }
+};
+// Never destroyed: its detached lanes wait on it until the process ends.
+inline Pool &pool = *new Pool;
+
+inline void fresh_block(unsigned threads, size_t lds) {
+    // Uninitialised LDS reads show as garbage, not as zeros.
+    std::memset(kh::lds, 0xA5, lds + 16);
+    delete block.all;
+    block.all = new std::barrier<>((ptrdiff_t)threads);
+    for (unsigned w = 0; w < 16; w++) {
+        delete block.wave[w];
+        block.wave[w] = w < threads / 64 ? new std::barrier<>(64) : nullptr;
+    }
+    block.threads = threads;
+}
+
+template <class K, class... A>
+void launch(K kernel, dim3 grid, dim3 threads, size_t lds, A... args) {
+    if (lds + 16 > LDS_BYTES || threads.x % 64 || threads.x > 1024 || threads.y != 1 || threads.z != 1) {
+        std::fprintf(stderr, "emu: launch shape not emulated (lds %zu, threads %u)\n", lds, threads.x);
+        std::abort();
+    }
+    const unsigned total = grid.x * grid.y * grid.z;
+    if (total == 0) return;
+    fresh_block(threads.x, lds);
+    // Between workgroups, the last lane to arrive makes the next one's barriers.
+    std::barrier<std::function<void()>> next((ptrdiff_t)threads.x,
+                                             std::function<void()>([&] { fresh_block(threads.x, lds); }));
+    pool.run(threads.x, [&](unsigned t) {
+        self.tid = dim3(t, 0, 0);
+        for (unsigned b = 0; b < total; b++) {
+            self.bid = dim3(b % grid.x, (b / grid.x) % grid.y, b / (grid.x * grid.y));
+            kernel(args...);
+            // A lane that ends leaves the barriers it no longer waits at.
+            block.wave[t / 64]->arrive_and_drop();
+            block.all->arrive_and_drop();
+            next.arrive_and_wait();
+        }
+    });
+}
+}  // namespace emu

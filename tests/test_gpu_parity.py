@@ -1,0 +1,307 @@
+"""Parity of the HIP path with the oracle (the restated CPU algorithm), on the
+device, through the C ABI.
+
+Bars (stated per test):
+- integer work bit-exact: activation bytes and scales (bytes.rs:144-158),
+  i32 block dots (bytes.rs:356-394), decoded weights (the f32 decoders of
+  quantized.rs:403-682);
+- f32 products within 1e-4 (1 + |e|) of the f64 product of the dequantized
+  weights (quantized.rs:1176-1179) and within the conformity tolerance
+  1e-4 max(1, max|y|) (conformity.rs:66, :1835-1840);
+- byte-activation products within 1e-5 sum|x_q w| + 1e-6 of the exact
+  product of the quantized activations (bytes.rs:753-770);
+- every result bitwise the same on a second run.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import kapel_amd as ka
+import oracle as ko
+from kapel_amd import synth
+from refrng import Rng, lcg_bytes
+
+pytestmark = pytest.mark.gpu
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+@pytest.fixture(scope="module")
+def hip():
+    return ka.Hip(0)
+
+
+def dev(a, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return t.to("cuda:0") if dtype is None else t.to("cuda:0", dtype)
+
+
+HALVES = {ka.Q8_0: [0], ka.Q4_0: [0], ka.Q5_0: [0], ka.Q4_1: [0, 2], ka.Q5_1: [0, 2],
+          ka.Q4K: [0, 2], ka.Q5K: [0, 2], ka.Q2K: [80, 82], ka.Q3K: [108], ka.Q6K: [208]}
+
+
+def random_blocks(fmt, group, count, seed):
+    """Random bytes with valid f16 scales (conformity.rs:601-635 / the
+    LCG of quantized.rs:1027-1062)."""
+    nxt = lcg_bytes(seed)
+    size = ko.block_bytes(fmt, group)
+    raw = np.frombuffer(bytes(nxt() for _ in range(count * size)), dtype=np.uint8).copy()
+    raw = raw.reshape(count, size)
+    rng = np.random.default_rng(seed)
+    for at in HALVES.get(fmt, []):
+        h = np.array([ko.f16_encode(v) for v in rng.uniform(0.005, 0.02, count)], dtype=np.uint16)
+        raw[:, at:at + 2] = h.view(np.uint8).reshape(count, 2)
+    if fmt in (ka.INT8, ka.INT4):
+        raw[:, :4] = np.frombuffer(rng.uniform(0.005, 0.02, count).astype(np.float32).tobytes(),
+                                   dtype=np.uint8).reshape(count, 4)
+    return raw.ravel()
+
+
+def weight(fmt, group, n, k, seed, hip):
+    data = random_blocks(fmt, group, n * k // ko.block_len(fmt, group), seed)
+    return data, ka.QuantizedTensor(dev(data), fmt, group, n, k)
+
+
+def x_uniform(rows, k, seed):
+    rng = Rng(seed)
+    return np.array([[rng.uniform(-1, 1) for _ in range(k)] for _ in range(rows)], np.float32)
+
+
+FORMATS = [(ka.INT8, 32), (ka.INT8, 64), (ka.INT8, 40), (ka.INT8, 128), (ka.INT4, 32),
+           (ka.INT4, 64), (ka.INT4, 128), (ka.INT4, 40), (ka.Q8_0, 0), (ka.Q4_0, 0), (ka.Q4_1, 0),
+           (ka.Q5_0, 0), (ka.Q5_1, 0), (ka.Q2K, 0), (ka.Q3K, 0), (ka.Q4K, 0), (ka.Q5K, 0),
+           (ka.Q6K, 0)]
+
+
+def check_f32(got, e64, what):
+    got = got.astype(np.float64)
+    bad = np.abs(got - e64) > 1e-4 * (1 + np.abs(e64))
+    assert not bad.any(), f"{what}: {np.argwhere(bad)[:3]} got {got[bad][:3]} want {e64[bad][:3]}"
+    scale = max(1.0, np.abs(e64).max()) if e64.size else 1.0
+    assert np.all(np.abs(got - e64) <= 1e-4 * scale), what
+
+
+@pytest.mark.parametrize("fmt,group", FORMATS)
+def test_products_of_every_format(hip, fmt, group):
+    """conformity.rs:877-935: [1 | 3 | 17, 1280] . fmt [7, 1280]^T, and the
+    oracle's f32 product (quantized.rs:117-175) alongside."""
+    k, n = 1280, 7
+    data, w = weight(fmt, group, n, k, 5 + fmt, hip)
+    for rows in (1, 3, 17):
+        x = x_uniform(rows, k, 100 + rows)
+        e64 = ko.product_f64([(fmt, group, data, n)], k, x)
+        cpu = ko.product_f32([(fmt, group, data, n)], k, x)
+        out = hip.forward(ka.QuantizedMatmul(), [dev(x), w])
+        got = out.cpu().numpy()
+        check_f32(got, e64, f"fmt {fmt}/{group} rows {rows}")
+        # The GPU and the CPU algorithm agree as closely as each does with f64.
+        assert np.all(np.abs(got - cpu) <= 2e-4 * (1 + np.abs(e64)))
+        again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_stacked_weights_of_several_formats(hip):
+    """conformity.rs:936-947: [q4_k 5; q6_k 3; q8_0 2] x 512, one output."""
+    k = 512
+    parts, ws = [], []
+    for i, (fmt, n) in enumerate(((ka.Q4K, 5), (ka.Q6K, 3), (ka.Q8_0, 2))):
+        data, w = weight(fmt, 0, n, k, 40 + i, hip)
+        parts.append((fmt, 0, data, n))
+        ws.append(w)
+    for rows in (1, 3, 17):
+        x = x_uniform(rows, k, rows)
+        e64 = ko.product_f64(parts, k, x)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x)] + ws).cpu().numpy()
+        assert got.shape == (rows, 10)
+        check_f32(got, e64, f"stacked rows {rows}")
+
+
+def test_empty_shapes(hip):
+    """conformity.rs:1414-1430: no rows, N = 0, K = 0 (zeros)."""
+    for fmt in (ka.INT8, ka.Q8_0):
+        group = 32 if fmt == ka.INT8 else 0
+        _, w = weight(fmt, group, 5, 64, 1, hip)
+        out = hip.forward(ka.QuantizedMatmul(), [torch.zeros((0, 64), device="cuda:0"), w])
+        assert out.shape == (0, 5)
+        empty = ka.QuantizedTensor(torch.zeros(0, dtype=torch.uint8, device="cuda:0"), fmt, group, 0, 64)
+        out = hip.forward(ka.QuantizedMatmul(), [torch.ones((3, 64), device="cuda:0"), empty])
+        assert out.shape == (3, 0)
+        k0 = ka.QuantizedTensor(torch.zeros(0, dtype=torch.uint8, device="cuda:0"), fmt, group, 5, 0)
+        out = hip.forward(ka.QuantizedMatmul(), [torch.ones((3, 0), device="cuda:0"), k0])
+        assert out.shape == (3, 5) and bool((out == 0).all())
+
+
+def test_activation_types(hip):
+    """bf16 and f16 activations give outputs of their type (the op's
+    signature), within the conformity tolerance of that type."""
+    k, n = 1024, 48
+    data, w = weight(ka.Q4K, 0, n, k, 9, hip)
+    x = x_uniform(2, k, 3)
+    for dtype, tol in ((torch.bfloat16, 5e-2), (torch.float16, 1e-2)):
+        xt = dev(x).to(dtype)
+        e64 = ko.product_f64([(ka.Q4K, 0, data, n)], k, xt.float().cpu().numpy())
+        got = hip.forward(ka.QuantizedMatmul(), [xt, w])
+        assert got.dtype == dtype
+        assert np.all(np.abs(got.float().cpu().numpy() - e64) <= tol * max(1, np.abs(e64).max()))
+
+
+BYTE_FORMATS = [(ka.Q8_0, 0), (ka.Q4_0, 0), (ka.Q4K, 0), (ka.Q5K, 0), (ka.Q6K, 0), (ka.INT8, 32),
+                (ka.INT8, 128), (ka.INT4, 32), (ka.INT4, 64)]
+
+
+def byte_x(rows, k):
+    i = np.arange(rows * k)
+    base = ((i * 7919) % 201).astype(np.float32) / np.float32(100.0) - np.float32(1.0)
+    return (base * (1 + (i // 32) % 7).astype(np.float32)).reshape(rows, k)
+
+
+def test_activation_bytes_are_bit_exact(hip):
+    """bytes.rs:144-158 on the device: q, scale and sums equal the oracle's
+    bit for bit, ties and zero blocks included."""
+    x = byte_x(6, 1024)
+    x[0, :32] = 0.0
+    x[1, :4] = [127.0, 0.5, 1.5, -2.5]
+    x[2, 64:96] = np.float32(1e-30)
+    q, s, sums = hip.quantize_x(dev(x))
+    oq, os_, osums = ko.quantize_x(x)
+    assert np.array_equal(q.cpu().numpy(), oq)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), os_.view(np.uint32))
+    assert np.array_equal(sums.cpu().numpy().view(np.uint32), osums.view(np.uint32))
+
+
+@pytest.mark.parametrize("fmt,group", BYTE_FORMATS)
+def test_byte_products_and_block_dots(hip, fmt, group):
+    """bytes.rs:720-774 plus the bit-exact i32 block dots."""
+    n, k = 13, 1024
+    data, w = weight(fmt, group, n, k, 3, hip)
+    for rows in (1, 6, 64):
+        x = byte_x(rows, k)
+        out_cpu, dots_cpu = ko.product_bytes([(fmt, group, data, n)], k, x, with_dots=True)
+        q, s, _ = ko.quantize_x(x)
+        dots = hip.block_dots(w, dev(q)).cpu().numpy()
+        assert np.array_equal(dots, dots_cpu), f"fmt {fmt} rows {rows}"
+        got = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w])
+        hip.with_byte_activations(False)
+        got = got.cpu().numpy().astype(np.float64)
+        dense = ko.dequantize(fmt, group, data).reshape(n, k)
+        xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+        e = xq @ dense.T
+        size = np.abs(xq) @ np.abs(dense).T
+        assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6), f"fmt {fmt} rows {rows}"
+        assert np.all(np.abs(got - out_cpu) <= 2e-5 * size + 2e-6)
+
+
+def test_byte_mode_falls_back_for_other_formats(hip):
+    """matmul.rs:293: one weight without a byte reader (Q2_K) puts the whole
+    product in f32 activations."""
+    k = 512
+    d1, w1 = weight(ka.Q4K, 0, 4, k, 1, hip)
+    d2, w2 = weight(ka.Q2K, 0, 4, k, 2, hip)
+    x = x_uniform(2, k, 9)
+    e64 = ko.product_f64([(ka.Q4K, 0, d1, 4), (ka.Q2K, 0, d2, 4)], k, x)
+    got = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w1, w2])
+    hip.with_byte_activations(False)
+    check_f32(got.cpu().numpy(), e64, "fallback")
+
+
+@pytest.mark.parametrize("fmt,group", FORMATS)
+def test_dequantize_matches_the_cpu_decoders(hip, fmt, group):
+    """kernels/src/lib.rs:3745 equivalent: the f32 values of the CPU's
+    portable decoders (quantized.rs:403-682), bit for bit, and gathered rows."""
+    n, k = 5, 512 if ko.block_len(fmt, group) != 40 else 520
+    data, w = weight(fmt, group, n, k, 21, hip)
+    got = hip.dequantize(w).cpu().numpy()
+    size, length = ko.block_bytes(fmt, group), ko.block_len(fmt, group)
+    want = np.concatenate([ko.decode_f32(fmt, group, data[i * size:(i + 1) * size])
+                           for i in range(n * k // length)]).reshape(n, k)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    rows = hip.dequantize_rows(w, torch.tensor([4, 0, 2, 2])).cpu().numpy()
+    assert np.array_equal(rows, want[[4, 0, 2, 2]])
+
+
+def test_golden_blocks_on_the_device(hip):
+    """The golden blocks of kapel-ref/src/golden.rs (tests/golden), decoded
+    on the device, within 1e-6 relative of their GGML-order values."""
+    with open(os.path.join(HERE, "golden", "golden_blocks.json")) as f:
+        cases = json.load(f)
+    for case in cases:
+        data = np.frombuffer(bytes.fromhex(case["bytes"]), dtype=np.uint8)
+        length = ko.block_len(case["format"], 0)
+        w = ka.QuantizedTensor(dev(data), case["format"], 0, 1, length)
+        got = hip.dequantize(w).cpu().numpy()[0].astype(np.float64)
+        want = np.array(case["values"])
+        assert np.all(np.abs(got - want) <= 1e-6 * np.maximum(np.abs(want), 1e-3)), case["name"]
+
+
+# ------------------------------------------------------------ full sizes
+
+LLAMA_3B = [("q", 3072, 3072, ka.Q4K), ("k", 1024, 3072, ka.Q4K), ("v", 1024, 3072, ka.Q4K),
+            ("o", 3072, 3072, ka.Q4K), ("gate", 8192, 3072, ka.Q4K), ("up", 8192, 3072, ka.Q4K),
+            ("down", 3072, 8192, ka.Q6K)]
+
+
+def synth_weight(fmt, group, n, k, seed):
+    values = synth.normal(seed, n * k, 0.02).reshape(n, k)
+    data = ka.quantize(fmt, group, values)
+    return data, ka.QuantizedTensor(dev(data), fmt, group, n, k)
+
+
+@pytest.mark.parametrize("byte", [False, True])
+def test_llama_3b_layer_at_full_size(hip, byte):
+    """Configs 2 and 3: each stacked call of the layer (qkv, o, gate+up, down)
+    at full size, M = 1 and M = 64 (bytes).  A sample of 96 output rows of
+    each matrix is checked against the oracle; every output is finite and a
+    second run is bitwise equal."""
+    rows = 64 if byte else 1
+    hip.with_byte_activations(byte)
+    try:
+        mats = {name: synth_weight(fmt, 0, n, k, 1000 + i) + (fmt, n, k)
+                for i, (name, n, k, fmt) in enumerate(LLAMA_3B)}
+        for call in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            k = mats[call[0]][4]
+            x = synth.normal(7, rows * k, 1.0).reshape(rows, k)
+            ws = [mats[c][1] for c in call]
+            got = hip.forward(ka.QuantizedMatmul(), [dev(x)] + ws).cpu().numpy()
+            again = hip.forward(ka.QuantizedMatmul(), [dev(x)] + ws).cpu().numpy()
+            assert np.isfinite(got).all()
+            assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+            col = 0
+            for c in call:
+                data, _, fmt, n, kk = mats[c]
+                sample = np.linspace(0, n - 1, 96).astype(int)
+                rb = ko.row_bytes(fmt, 0, kk)
+                sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
+                xr = x[: min(rows, 8)]
+                if byte:
+                    want = ko.product_bytes([(fmt, 0, sub, len(sample))], kk, xr)
+                    q, s, _ = ko.quantize_x(xr)
+                    dense = ko.dequantize(fmt, 0, sub).reshape(len(sample), kk)
+                    xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+                    size = np.abs(xq) @ np.abs(dense).T
+                    assert np.all(np.abs(got[: len(xr), col + sample] - want) <= 2e-5 * size + 2e-6), c
+                else:
+                    e64 = ko.product_f64([(fmt, 0, sub, len(sample))], kk, xr)
+                    check_f32(got[: len(xr), col + sample], e64, c)
+                col += n
+    finally:
+        hip.with_byte_activations(False)
+
+
+def test_low_bit_mix_and_output_table_sample(hip):
+    """Config 5 shapes at M in {1, 8}: Q2_K/Q3_K/Q5_K FFN matrices, int4/32
+    attention, Q6_K output-table rows (a slice of 4096 rows of the table)."""
+    cases = [(ka.Q2K, 0, 12288, 4096), (ka.Q3K, 0, 4096, 12288), (ka.Q5K, 0, 12288, 4096),
+             (ka.INT4, 32, 4096, 4096), (ka.Q6K, 0, 4096, 4096)]
+    for i, (fmt, group, n, k) in enumerate(cases):
+        data, w = synth_weight(fmt, group, n, k, 2000 + i)
+        for rows in (1, 8):
+            x = synth.normal(50 + rows, rows * k, 1.0).reshape(rows, k)
+            got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+            sample = np.linspace(0, n - 1, 64).astype(int)
+            rb = ko.row_bytes(fmt, group, k)
+            sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
+            e64 = ko.product_f64([(fmt, group, sub, len(sample))], k, x)
+            check_f32(got[:, sample], e64, f"fmt {fmt} rows {rows}")

@@ -544,3 +544,16 @@ def test_products_are_those_of_the_activations_in_bytes(fmt, group):
     # Results do not depend on the thread count.
     again = ko.product_bytes([(fmt, group, w, n)], k, x, threads=1)
     assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
+
+
+def test_golden_fixture_matches_the_oracle():
+    """tests/golden/golden_blocks.json (written by make_golden.py from the
+    GGML transcriptions above) decodes exactly under the oracle."""
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "golden_blocks.json")) as f:
+        cases = json.load(f)
+    assert len(cases) == 8
+    for case in cases:
+        data = np.frombuffer(bytes.fromhex(case["bytes"]), dtype=np.uint8)
+        same(ko.dequantize(case["format"], 0, data), case["values"])
