@@ -105,8 +105,9 @@ uint64_t kh_qmatmul_workspace(const kh_weight *weights, uint32_t count, uint64_t
 
 /* out [rows, sum n] = x [rows, k] . [w_1; w_2; ...]^T, out in `out_kind`
  * (the activations' type, as the op's signature says).  x and out are
- * contiguous device arrays.  `workspace` (device, kh_qmatmul_workspace
- * bytes) must be zero-filled before its first use; every call leaves it in a
+ * contiguous device arrays; weight data 4-byte aligned.  `workspace`
+ * (device, kh_qmatmul_workspace bytes, 256-byte aligned) must be zero-filled
+ * before its first use; every call leaves it in a
  * state the next call accepts.  Calls that share a workspace must be ordered
  * (one stream).  Results are bitwise the same from run to run: every
  * reduction is split by the shapes only.

@@ -92,18 +92,20 @@ Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
     return Split{segs, seg_steps, lds_bytes(rows, planes, seg_steps)};
 }
 
-// The workspace: the prepared activations, then the partial sums and the
-// counters of the segment split.
+// The workspace: the counters of the segment split (fixed, first), the
+// prepared activations, then the partial sums.
 struct Layout {
     uint64_t kpad;
-    uint64_t planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off;
-    uint64_t partials_off, counters_off, total;
+    uint64_t counters_off, planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off;
+    uint64_t partials_off, total;
 };
 
-Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats, uint64_t max_wgs) {
+Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats) {
     Layout l{};
     l.kpad = align_up(std::max<uint64_t>(k, 64), 64);
     uint64_t at = 0;
+    l.counters_off = at;
+    at = align_up(at + MAX_COUNTERS * 4, 256);
     l.planes_off = at;
     at = align_up(at + rows * planes * l.kpad, 256);
     l.xscale_off = at;
@@ -117,8 +119,6 @@ Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats, ui
     l.partials_off = at;
     // Partial sums of the largest launch: segments x rows x columns.
     at = align_up(at + partial_floats * 4, 256);
-    l.counters_off = at;
-    at = align_up(at + (max_wgs + 1) * 4, 256);
     l.total = at;
     return l;
 }
@@ -186,6 +186,9 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
         if (w.n > (1ull << 31)) return KH_ERR_OVERFLOW;
         if (w.bytes != w.n * (k / len) * size) return KH_ERR_SHAPE;
         if (w.n && k && !w.data) return KH_ERR_NULL;
+        // Rows are read with 4-byte loads (kapel-cuda/src/quantized.rs:123-129
+        // asks the same of its fast kernels).
+        if ((uintptr_t)w.data & 3u) return KH_ERR_SHAPE;
         uint64_t sum = c.width + w.n;
         if (sum < c.width) return KH_ERR_OVERFLOW;
         c.width = sum;
@@ -195,6 +198,7 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
     if (c.width > (1ull << 31)) return KH_ERR_OVERFLOW;
     c.bytes = (flags & KH_BYTE_ACTIVATIONS) && all_bytes;
     c.max_wgs = div_up(tiles, 4) + count;
+    if (c.max_wgs > MAX_COUNTERS) return KH_ERR_OVERFLOW;
     if (k > 0 && rows > 0)
         each_launch(weights, count, k, rows, c.bytes ? 1 : 3, [&](const Launch &L) {
             if (L.split.segs > 1)
@@ -349,7 +353,7 @@ uint64_t kh_qmatmul_workspace(const kh_weight *weights, uint32_t count, uint64_t
                               uint32_t flags) {
     Checked c;
     if (check(weights, count, k, rows, flags, c) != KH_OK) return 0;
-    return layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.max_wgs).total;
+    return layout(rows, k, c.bytes ? 1 : 3, c.partial_floats).total;
 }
 
 int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
@@ -370,8 +374,9 @@ int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_
                    : KH_ERR_HIP;
     }
     if (!x) return KH_ERR_NULL;
-    Layout l = layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.max_wgs);
-    if (!workspace || workspace_bytes < l.total) return KH_ERR_WORKSPACE;
+    Layout l = layout(rows, k, c.bytes ? 1 : 3, c.partial_floats);
+    if (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255u))
+        return KH_ERR_WORKSPACE;
     hipError_t err = plan_and_launch(weights, count, k, x_kind, x, rows, out_kind, out, c,
                                      static_cast<uint8_t *>(workspace), l,
                                      (flags & KH_REUSE_ACTIVATIONS) != 0, s);
@@ -405,8 +410,9 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     if (!c.bytes) return KH_ERR_DTYPE;
     if (rows == 0 || weight->n == 0 || k == 0) return KH_OK;
     if (!q || !dots) return KH_ERR_NULL;
-    Layout l = layout(rows, k, 1, c.partial_floats, c.max_wgs);
-    if (!workspace || workspace_bytes < l.total) return KH_ERR_WORKSPACE;
+    Layout l = layout(rows, k, 1, c.partial_floats);
+    if (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255u))
+        return KH_ERR_WORKSPACE;
     uint8_t *ws = static_cast<uint8_t *>(workspace);
     hipStream_t s = static_cast<hipStream_t>(stream);
     PrepArgs p{};

@@ -28,20 +28,35 @@ namespace kh {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 
-// Loads.  Block starts of 18-, 34-, 110- and 210-byte formats are only
-// 2-byte aligned: gfx950 global loads take unaligned dword addresses.
-__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {
-    return *reinterpret_cast<const uint32_t *>(p);
-}
-__device__ __forceinline__ uint16_t ld16(const uint8_t *p) {
+// Loads.  Every load reads exactly its bytes at their natural alignment:
+// blocks of 18, 22, 34, 110 and 210 bytes start at even addresses only, and
+// Kapel's groups of odd size at any address.
+__device__ __forceinline__ uint16_t ld16(const uint8_t *p) {  // p even
     return *reinterpret_cast<const uint16_t *>(p);
 }
-__device__ __forceinline__ uint2 ld64(const uint8_t *p) {
-    return *reinterpret_cast<const uint2 *>(p);
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p a multiple of 4
+    return *reinterpret_cast<const uint32_t *>(p);
 }
-__device__ __forceinline__ float ldf32(const uint8_t *p) {
-    return __uint_as_float(ld32(p));
+__device__ __forceinline__ uint2 ld64(const uint8_t *p) {  // p a multiple of 4
+    if (((uintptr_t)p & 7u) == 0) return *reinterpret_cast<const uint2 *>(p);
+    return uint2{ld32(p), ld32(p + 4)};
 }
+// p even.
+__device__ __forceinline__ uint32_t ld32e(const uint8_t *p) {
+    if (((uintptr_t)p & 3u) == 0) return ld32(p);
+    return (uint32_t)ld16(p) | ((uint32_t)ld16(p + 2) << 16);
+}
+__device__ __forceinline__ uint2 ld64e(const uint8_t *p) {
+    if (((uintptr_t)p & 3u) == 0) return ld64(p);
+    uint32_t mid = ld32(p + 2);
+    return uint2{(uint32_t)ld16(p) | (mid << 16), (mid >> 16) | ((uint32_t)ld16(p + 6) << 16)};
+}
+// Any address.
+__device__ __forceinline__ uint32_t ld32b(const uint8_t *p) {
+    if (((uintptr_t)p & 3u) == 0) return ld32(p);
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+__device__ __forceinline__ float ldf32(const uint8_t *p) { return __uint_as_float(ld32b(p)); }
 
 // IEEE half to f32, exactly, with integer operations only (independent of
 // the denormal mode): kapel-cpu/src/quantized.rs:386-396 gives the same value.
@@ -127,8 +142,8 @@ struct Q6K {
     __device__ static v4i codes(const uint8_t *row, int t, int g, bool) {
         const uint8_t *blk = row + (t >> 2) * BYTES;
         int h = (t >> 1) & 1, l0 = 16 * (t & 1) + 4 * g;
-        uint32_t a0 = ld32(blk + h * 64 + l0), a1 = ld32(blk + h * 64 + 32 + l0);
-        uint32_t q = ld32(blk + 128 + h * 32 + l0);
+        uint32_t a0 = ld32e(blk + h * 64 + l0), a1 = ld32e(blk + h * 64 + 32 + l0);
+        uint32_t q = ld32e(blk + 128 + h * 32 + l0);
         return v4i{(int)((a0 & LO4) | ((q << 4) & 0x30303030u)),
                    (int)((a1 & LO4) | ((q << 2) & 0x30303030u)),
                    (int)(((a0 >> 4) & LO4) | (q & 0x30303030u)),
@@ -180,7 +195,7 @@ struct Q3K {
     __device__ static v4i codes(const uint8_t *row, int t, int g, bool) {
         const uint8_t *blk = row + (t >> 2) * BYTES;
         int h = (t >> 1) & 1, l0 = 16 * (t & 1) + 4 * g;
-        uint32_t q = ld32(blk + 32 + h * 32 + l0), mk = ld32(blk + l0) >> (4 * h);
+        uint32_t q = ld32e(blk + 32 + h * 32 + l0), mk = ld32e(blk + l0) >> (4 * h);
         return v4i{(int)((q & 0x03030303u) | ((mk << 2) & 0x04040404u)),
                    (int)(((q >> 2) & 0x03030303u) | ((mk << 1) & 0x04040404u)),
                    (int)(((q >> 4) & 0x03030303u) | (mk & 0x04040404u)),
@@ -221,8 +236,8 @@ struct Q4_0 {
     static constexpr int LEN = 32, BYTES = 18, NGRP = 2, GS = 32;
     __device__ static v4i codes(const uint8_t *row, int t, int g, bool two) {
         const uint8_t *b0 = row + 2 * t * BYTES;
-        return join(nib32(ld32(b0 + 2 + 4 * g)),
-                    two ? nib32(ld32(b0 + BYTES + 2 + 4 * g)) : int2{0, 0});
+        return join(nib32(ld32e(b0 + 2 + 4 * g)),
+                    two ? nib32(ld32e(b0 + BYTES + 2 + 4 * g)) : int2{0, 0});
     }
     __device__ static int xoff(int t, int g, int d) { return xoff_nib32(t, g, d); }
     __device__ static int gelem(int t, int grp) { return 64 * t + 32 * grp; }
@@ -259,7 +274,7 @@ template <int OFFSET, bool MIN>
 struct Q5x {
     static constexpr int LEN = 32, BYTES = MIN ? 24 : 22, NGRP = 2, GS = 32;
     __device__ static int2 one(const uint8_t *blk, int g) {
-        uint32_t high = ld32(blk + OFFSET), w = ld32(blk + OFFSET + 4 + 4 * g);
+        uint32_t high = ld32e(blk + OFFSET), w = ld32e(blk + OFFSET + 4 + 4 * g);
         return int2{(int)((w & LO4) | spread4(high, 4 * g)),
                     (int)(((w >> 4) & LO4) | spread4(high, 16 + 4 * g))};
     }
@@ -283,8 +298,8 @@ struct Q8_0 {
     static constexpr int LEN = 32, BYTES = 34, NGRP = 2, GS = 32;
     __device__ static v4i codes(const uint8_t *row, int t, int g, bool two) {
         const uint8_t *b0 = row + 2 * t * BYTES;
-        uint2 a = ld64(b0 + 2 + 8 * g);
-        uint2 b = two ? ld64(b0 + BYTES + 2 + 8 * g) : uint2{0u, 0u};
+        uint2 a = ld64e(b0 + 2 + 8 * g);
+        uint2 b = two ? ld64e(b0 + BYTES + 2 + 8 * g) : uint2{0u, 0u};
         return v4i{(int)a.x, (int)a.y, (int)b.x, (int)b.y};
     }
     __device__ static int xoff(int t, int g, int d) { return xoff_seq32(t, g, d); }

@@ -18,6 +18,10 @@ constexpr int MAX_MFMAS = 8;
 constexpr int slot_groups_per_mfma(int planes) { return planes == 3 ? 4 : 16; }
 // Segments of K at most.
 constexpr int MAX_SEGS = 64;
+// Counters of the segment split: at the start of every workspace, a region
+// no call uses for anything else, so that the zeros each launch leaves behind
+// are there for the next call whatever its shapes.
+constexpr uint64_t MAX_COUNTERS = 1u << 16;
 // LDS of one workgroup of the product at most.
 constexpr int MAX_LDS = 64 * 1024;
 

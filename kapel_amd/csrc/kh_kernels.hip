@@ -407,7 +407,7 @@ __device__ float element(uint32_t fmt, uint32_t group, const uint8_t *row, uint6
         bool one = fmt == KH_Q5_1;
         const uint8_t *blk = row + (e / 32) * (one ? 24 : 22);
         const uint8_t *rest = blk + (one ? 4 : 2);
-        uint32_t j = e % 32, high = ld32(rest), byte = rest[4 + j % 16];
+        uint32_t j = e % 32, high = ld32e(rest), byte = rest[4 + j % 16];
         uint32_t q = (j < 16 ? byte & 15u : byte >> 4) | (((high >> j) & 1u) << 4);
         return one ? half_at(blk) * (float)q + half_at(blk + 2) : half_at(blk) * ((float)q - 16.0f);
     }

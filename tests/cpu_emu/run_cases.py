@@ -62,12 +62,29 @@ def xs(rows, k, seed):
     return np.array([[rng.uniform(-1, 1) for _ in range(k)] for _ in range(rows)], np.float32)
 
 
+def aligned(nbytes):
+    """A zeroed byte buffer at a 256-byte aligned address."""
+    raw = np.zeros(nbytes + 256, np.uint8)
+    off = (-raw.ctypes.data) % 256
+    return raw[off:off + nbytes]
+
+
+# One workspace for every case, as a caller keeps one: each call must leave it
+# ready for the next, whatever the shapes.
+WORKSPACE = aligned(64 << 20)
+
+
+def workspace(size):
+    assert size <= WORKSPACE.size
+    return WORKSPACE
+
+
 def product(parts, k, x, flags=0):
     arr = (W * len(parts))(*[W(f, g, d.ctypes.data, d.size, n) for f, g, d, n in parts])
     rows = x.shape[0]
     width = sum(p[3] for p in parts)
     size = L.kh_qmatmul_workspace(arr, len(parts), k, rows, flags)
-    ws = np.zeros(max(size, 1), np.uint8)
+    ws = workspace(size)
     out = np.full((rows, width), np.nan, np.float32)
     st = L.kh_qmatmul(arr, len(parts), k, F32, x.ctypes.data, rows, F32, out.ctypes.data, flags,
                       ws.ctypes.data, ws.size, None)
@@ -103,7 +120,7 @@ def case_bytes(fmt, group, n, k, rows):
     q, s, _ = ko.quantize_x(x)
     w = W(fmt, group, d.ctypes.data, d.size, n)
     size = L.kh_qmatmul_workspace(ctypes.byref(w), 1, k, rows, 1)
-    ws = np.zeros(max(size, 1), np.uint8)
+    ws = workspace(size)
     dots = np.zeros((rows, n, k // 16), np.int32)
     assert L.kh_block_dots(ctypes.byref(w), k, q.ctypes.data, rows, dots.ctypes.data,
                            ws.ctypes.data, ws.size, None) == 0
@@ -130,7 +147,7 @@ def case_kinds():
             xb = x.astype(np.float16).view(np.uint16)
             xf = xb.view(np.float16).astype(np.float32)
         size = L.kh_qmatmul_workspace(w, 1, k, 2, 0)
-        ws = np.zeros(size, np.uint8)
+        ws = workspace(size)
         out = np.zeros((2, n), np.uint16)
         assert L.kh_qmatmul(w, 1, k, kind, xb.ctypes.data, 2, kind, out.ctypes.data, 0,
                             ws.ctypes.data, ws.size, None) == 0
@@ -180,6 +197,9 @@ BYTE_FORMATS = [(Q8_0, 0), (Q4_0, 0), (Q4K, 0), (Q5K, 0), (Q6K, 0), (INT8, 32), 
 
 def main(which):
     case_product(INT8, 32, 7, 1280, 1)  # the first case of the GPU tests
+    for rows in (1, 3, 17):             # then more rows, then another shape
+        case_product(INT8, 32, 7, 1280, rows)
+    case_product(INT8, 64, 7, 1280, 1)
     case_quantize_x()
     case_kinds()
     for fmt, group in FORMATS:

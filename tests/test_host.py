@@ -104,12 +104,13 @@ def test_quantizer_refuses_partial_blocks():
         ka.quantize(ka.IQ3_S, 0, np.zeros(256, np.float32))
 
 
-def weight_struct(fmt, group, n, k, data=1):
+def weight_struct(fmt, group, n, k, data=4096):
     size = 0 if ka.block_len(fmt, group) == 0 else k // max(1, ka.block_len(fmt, group)) * ka.block_bytes(fmt, group) * n
     return ka._Weight(fmt, group, data, size, n)
 
 
-def qmatmul(weights, k, rows, x=1, out=1, kind=ka.F32, flags=0, ws=1, ws_bytes=1 << 40):
+def qmatmul(weights, k, rows, x=4096, out=4096, kind=ka.F32, flags=0, ws=4096, ws_bytes=1 << 40):
+    """Fake, aligned addresses: every call here is refused or empty before any access."""
     arr = (ka._Weight * max(1, len(weights)))(*weights)
     return ka.lib().kh_qmatmul(arr, len(weights), k, kind, x, rows, kind, out, flags, ws,
                                ws_bytes, None)
@@ -121,12 +122,14 @@ def test_the_abi_refuses_what_infer_refuses():
     assert qmatmul([], 512, 1) == ka.KH_ERR_ARITY
     assert qmatmul([weight_struct(99, 0, 4, 512)], 512, 1) == ka.KH_ERR_DTYPE
     assert qmatmul([weight_struct(ka.Q4K, 0, 4, 512)], 500, 1) == ka.KH_ERR_MISALIGNED
-    bad = ka._Weight(ka.Q4K, 0, 1, 7, 4)
+    bad = ka._Weight(ka.Q4K, 0, 4096, 7, 4)
     assert qmatmul([bad], 512, 1) == ka.KH_ERR_SHAPE
     assert qmatmul([w], 512, 1, kind=7) == ka.KH_ERR_DTYPE
     assert qmatmul([w], 512, 1, ws=None) == ka.KH_ERR_WORKSPACE
     assert qmatmul([w], 512, 1, ws_bytes=16) == ka.KH_ERR_WORKSPACE
-    huge = ka._Weight(ka.Q4K, 0, 1, (1 << 33) * 144, 1 << 33)
+    assert qmatmul([w], 512, 1, ws=4096 + 64) == ka.KH_ERR_WORKSPACE  # 256-byte alignment
+    assert qmatmul([weight_struct(ka.Q4K, 0, 4, 512, data=4098)], 512, 1) == ka.KH_ERR_SHAPE
+    huge = ka._Weight(ka.Q4K, 0, 4096, (1 << 33) * 144, 1 << 33)
     assert qmatmul([huge], 256, 1) == ka.KH_ERR_OVERFLOW
     assert qmatmul([w], 512, 1, x=None) == ka.KH_ERR_NULL
     # Nothing to do: no rows, or no weight rows.
