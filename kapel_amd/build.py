@@ -30,17 +30,23 @@ def _run(cmd):
 def build(verbose=False):
     objdir = os.path.join(HERE, "_build")
     os.makedirs(objdir, exist_ok=True)
-    objs = []
-    for src, compiler, flags in (
+    units = (
         ("kh_kernels.hip", HIPCC, HIP_FLAGS),
+        ("kh_gemv.hip", HIPCC, HIP_FLAGS),
         ("kh_api.cpp", HIPCC, HIP_FLAGS),
         ("kh_quantize.cpp", "g++", HOST_FLAGS),
-    ):
-        obj = os.path.join(objdir, src + ".o")
-        _run([compiler, *flags, "-c", os.path.join(CSRC, src), "-o", obj])
-        objs.append(obj)
+    )
+    objs = [os.path.join(objdir, src + ".o") for src, _, _ in units]
+
+    def compile_one(i):
+        src, compiler, flags = units[i]
+        _run([compiler, *flags, "-c", os.path.join(CSRC, src), "-o", objs[i]])
         if verbose:
             print("compiled", src)
+
+    from concurrent.futures import ThreadPoolExecutor
+    with ThreadPoolExecutor(len(units)) as pool:
+        list(pool.map(compile_one, range(len(units))))
     tmp = OUT + ".tmp"
     _run([HIPCC, "--offload-arch=" + ARCH, "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, OUT)

@@ -9,6 +9,7 @@
 
 #include <algorithm>
 #include <cstdint>
+#include <cstdlib>
 #include <cstring>
 #include <vector>
 
@@ -92,6 +93,27 @@ Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
     return Split{segs, seg_steps, lds_bytes(rows, planes, seg_steps)};
 }
 
+// The small-M product: activation rows it takes in one launch.
+int gemv_max_rows(int planes) { return planes == 1 ? 16 : 8; }
+
+// Its split: tiles per workgroup (4, 2 or 1; as many as leave a workgroup
+// for each of the 256 CUs), waves per tile (4 / tiles) splitting K, and
+// chunks of K of at most 8192 activations (rows x chunk) prepared at a time.
+// A function of the shapes only.
+struct GemvSplit {
+    int units, chunk, tiles, kw;
+};
+
+GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows) {
+    GemvSplit g{};
+    g.units = (int)div_up(k, unit);
+    g.tiles = 4;
+    while (g.tiles > 1 && div_up(tiles, g.tiles) < 256) g.tiles /= 2;
+    g.kw = 4 / g.tiles;
+    g.chunk = std::max(1, std::min(g.units, 8192 / (rows * unit)));
+    return g;
+}
+
 // The workspace: the counters of the segment split (fixed, first), the
 // prepared activations, then the partial sums.
 struct Layout {
@@ -126,6 +148,7 @@ Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats) {
 struct Checked {
     uint64_t width = 0, max_wgs = 0, partial_floats = 0;
     bool bytes = false;
+    bool any_qmv = false;  // a launch of the many-row product (prepared activations)
 };
 
 // One launch of the MFMA product: weights `members` (one format), rows
@@ -135,6 +158,8 @@ struct Launch {
     int tiles;
     uint64_t r0;
     int rows;
+    bool gemv;        // the small-M product (all rows in one launch)
+    GemvSplit gsplit;
     Split split;
 };
 
@@ -161,6 +186,16 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         for (uint32_t m : L.members) L.tiles += (int)div_up(weights[m].n, 16);
         if (L.tiles == 0) continue;
         int steps = (int)div_up(k, 64);
+        int unit = gemv_unit(w.format, w.group);
+        if (unit && rows <= (uint64_t)gemv_max_rows(planes)) {
+            L.gemv = true;
+            L.r0 = 0;
+            L.rows = (int)rows;
+            L.gsplit = gemv_split(k, unit, L.tiles, L.rows);
+            fn(L);
+            continue;
+        }
+        L.gemv = false;
         int chunk = rows_per_launch(w.format, planes);
         for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
             L.r0 = r0;
@@ -201,6 +236,8 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
     if (c.max_wgs > MAX_COUNTERS) return KH_ERR_OVERFLOW;
     if (k > 0 && rows > 0)
         each_launch(weights, count, k, rows, c.bytes ? 1 : 3, [&](const Launch &L) {
+            if (L.gemv) return;
+            c.any_qmv = true;
             if (L.split.segs > 1)
                 c.partial_floats = std::max<uint64_t>(
                     c.partial_floats, (uint64_t)L.split.segs * L.rows * L.tiles * 16);
@@ -215,9 +252,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     int planes = c.bytes ? 1 : 3;
     hipError_t err;
     // The activations, once for all weights.
-    bool any_mfma = false;
-    for (uint32_t i = 0; i < count; i++) any_mfma |= mfma_format(weights[i].format, weights[i].group);
-    if (any_mfma && !reuse) {
+    if (c.any_qmv && !reuse) {
         PrepArgs p{};
         p.x_kind = x_kind;
         p.x = x;
@@ -262,6 +297,37 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     each_launch(weights, count, k, rows, planes, [&](const Launch &L) {
         if (err != hipSuccess) return;
         const kh_weight &w = weights[L.members[0]];
+        if (L.gemv) {
+            GemvArgs a{};
+            a.count = (int)L.members.size();
+            int tiles = 0;
+            for (int m = 0; m < a.count; m++) {
+                const kh_weight &wm = weights[L.members[m]];
+                a.w[m] = static_cast<const uint8_t *>(wm.data);
+                a.n[m] = wm.n;
+                a.col0[m] = col0[L.members[m]];
+                a.tile0[m] = tiles;
+                tiles += (int)div_up(wm.n, 16);
+            }
+            uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+            a.row_bytes = k / len * size;
+            a.k = (int)k;
+            a.units = L.gsplit.units;
+            a.chunk = L.gsplit.chunk;
+            a.total_tiles = tiles;
+            a.tiles = L.gsplit.tiles;
+            a.kw = L.gsplit.kw;
+            a.rows = L.rows;
+            a.x_kind = x_kind;
+            a.x = x;
+            a.x_vec = ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) == 0;
+            a.out_kind = out_kind;
+            a.out = out;
+            a.out_stride = c.width;
+            a.width = c.width;
+            err = launch_gemv(w.format, w.group, planes, a, s);
+            return;
+        }
         QmvArgs a{};
         a.count = (int)L.members.size();
         int tiles = 0;
@@ -297,7 +363,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
         dim3 grid((unsigned)div_up(tiles, 4), (unsigned)L.split.segs);
         err = launch_qmv(w.format, w.group, planes, a, grid, L.split.lds, s);
     });
-    return hipSuccess;
+    return err;
 }
 
 }  // namespace
@@ -426,8 +492,32 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     p.xsum32 = reinterpret_cast<float *>(ws + l.xsum32_off);
     p.xsum16 = reinterpret_cast<float *>(ws + l.xsum16_off);
     p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
-    if (launch_prep(p, s) != hipSuccess) return KH_ERR_HIP;
     const kh_weight &w = *weight;
+    int unit = gemv_unit(w.format, w.group);
+    if (unit && rows <= (uint64_t)gemv_max_rows(1)) {
+        // The bytes go through the small-M product's own preparation.
+        GemvArgs g{};
+        g.count = 1;
+        g.w[0] = static_cast<const uint8_t *>(w.data);
+        g.n[0] = w.n;
+        uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+        g.row_bytes = k / len * size;
+        g.k = (int)k;
+        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), (int)rows);
+        g.units = sp.units;
+        g.chunk = sp.chunk;
+        g.total_tiles = (int)div_up(w.n, 16);
+        g.tiles = sp.tiles;
+        g.kw = sp.kw;
+        g.rows = (int)rows;
+        g.x_kind = KH_I8_INTERNAL;
+        g.x = q;
+        g.x_vec = 0;
+        g.dots = dots;
+        g.width = w.n;
+        return launch_gemv(w.format, w.group, 1, g, s) == hipSuccess ? KH_OK : KH_ERR_HIP;
+    }
+    if (launch_prep(p, s) != hipSuccess) return KH_ERR_HIP;
     QmvArgs a{};
     a.count = 1;
     a.w[0] = static_cast<const uint8_t *>(w.data);

@@ -7,6 +7,10 @@
 
 namespace kh {
 
+// Activations already in bytes (kh_block_dots): the small-M product takes
+// them as its plane, with scale 1.
+constexpr uint32_t KH_I8_INTERNAL = 0x100u;
+
 // Weights per launch of the product (stacked matrices of one format).
 constexpr int MAX_WEIGHTS = 8;
 // MFMAs per step at most: 8 x 4 slot groups with f32 activations, 8 x 16
@@ -69,6 +73,30 @@ struct QmvArgs {
     int signed_offset;
 };
 
+// The small-M product (kh_gemv.hip): weights of one format in tiles of 16
+// rows; a workgroup takes `tiles` tiles with `kw` waves each, the waves of a
+// tile splitting K; K is walked in chunks of `chunk` units whose activations
+// the workgroup prepares in LDS.
+struct GemvArgs {
+    int count;
+    const uint8_t *w[MAX_WEIGHTS];
+    uint64_t n[MAX_WEIGHTS];
+    uint64_t col0[MAX_WEIGHTS];
+    int tile0[MAX_WEIGHTS];
+    uint64_t row_bytes;
+    int k, units, chunk;
+    int total_tiles, tiles, kw;
+    int rows;                     // activation rows
+    uint32_t x_kind;
+    const void *x;                // [rows, k]
+    int x_vec;                    // x may be read 4 elements at a time
+    uint32_t out_kind;
+    void *out;                    // [rows, out_stride]
+    uint64_t out_stride;
+    int32_t *dots;                // block dots [rows, width, k / 16] instead of out
+    uint64_t width;
+};
+
 struct GenericArgs {
     uint32_t format, group;
     const uint8_t *w;
@@ -94,6 +122,11 @@ hipError_t launch_fill(uint32_t *p, uint64_t words, hipStream_t s);
 hipError_t launch_fill_bytes(uint8_t *p, uint64_t bytes, hipStream_t s);
 hipError_t launch_qmv(uint32_t fmt, uint32_t group, int planes, const QmvArgs &a, dim3 grid,
                       size_t lds, hipStream_t s);
+// Units of the small-M product for a format (0: not read by it).
+int gemv_unit(uint32_t fmt, uint32_t group);
+// Bytes of LDS of one of its workgroups.
+size_t gemv_lds(int rows, int planes, int chunk, int unit, int waves);
+hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s);
 hipError_t launch_generic(const GenericArgs &a, hipStream_t s);
 hipError_t launch_dequantize(const DequantArgs &a, hipStream_t s);
 

@@ -1,0 +1,423 @@
+// Lane readers of the quantized formats for the small-M product (kh_gemv.hip).
+//
+// A wave takes 16 weight rows; lane l serves row n = l % 16 as "lane group"
+// g = l / 16.  The product walks a row by units (256 elements for the
+// 256-element super-blocks, 128 for the 32-element blocks and Kapel's
+// int8/int4 groups).  In a unit, each lane group owns its own elements: for
+// every MFMA step s the 16 codes a lane gives as B operand of
+// v_mfma_i32_16x16x64_i8 are 16 elements of ONE scale group of that lane
+// group, and the activations (A operand) of that step are the 16 elements at
+// unit offset xpos(g, s), consecutive.  Each lane therefore gets back in C
+// exactly the dots of its own groups and applies their scales itself.
+//
+// A reader loads its lane's bytes with the widest loads the alignment allows
+// (16-byte loads at 4-byte-aligned addresses; formats whose blocks start at
+// even addresses only are read from the 4-byte-aligned address below and put
+// back in place with v_alignbyte), never touching a byte outside the unit.
+// Scales and minimums are the f32 products of the CPU decoders
+// (kapel-cpu/src/quantized.rs:403-682, k_scales :603-616); element layouts
+// follow kapel-core/src/dtype.rs:342-520.
+#pragma once
+#include <hip/hip_fp16.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace kh {
+namespace lanes {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr uint32_t LO4 = 0x0f0f0f0fu;
+
+// ---------------------------------------------------------------- loads
+__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p % 4 == 0
+    return *reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
+}
+__device__ __forceinline__ uint32_t ld16(const uint8_t *p) {  // p % 2 == 0
+    return *reinterpret_cast<const uint16_t *>(__builtin_assume_aligned(p, 2));
+}
+// N dwords at a 4-byte-aligned address (merged into 16-byte loads).
+template <int N>
+__device__ __forceinline__ void ldw(uint32_t (&v)[N], const uint8_t *p) {
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = q[i];
+}
+
+// The bytes [p, p + R) of an even address p, as ceil(R / 4) dwords in
+// place.  Loads from p - (p % 4): the two bytes below p belong to the
+// tensor (a tensor starts at a multiple of 4), and nothing at or beyond
+// p + R is read.
+template <int R>
+__device__ __forceinline__ void run(uint32_t (&w)[(R + 3) / 4], const uint8_t *p) {
+    static_assert(R % 2 == 0, "even runs only");
+    constexpr int F = R / 4, W = (R + 3) / 4;
+    const uint32_t s = (uint32_t)(uintptr_t)p & 2u;
+    const uint8_t *a = p - s;
+    uint32_t v[F + 2];
+    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(a, 4));
+#pragma unroll
+    for (int i = 0; i < F; i++) v[i] = q[i];
+    if (R % 4 == 2) v[F] = s ? q[F] : ld16(a + 4 * F);
+    else v[F] = s ? ld16(a + 4 * F) : 0u;
+    v[F + 1] = 0u;
+#pragma unroll
+    for (int i = 0; i < W; i++) v[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], s);
+#pragma unroll
+    for (int i = 0; i < W; i++) w[i] = v[i];
+}
+
+__device__ __forceinline__ float f16(uint32_t h) { return __half2float(__ushort_as_half((uint16_t)h)); }
+__device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
+// Dword i of a 16-byte vector held as four dwords.
+__device__ __forceinline__ v4i vec(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+    return v4i{(int)a, (int)b, (int)c, (int)d};
+}
+__device__ __forceinline__ v4i lo4(const uint32_t *q) {
+    return vec(q[0] & LO4, q[1] & LO4, q[2] & LO4, q[3] & LO4);
+}
+__device__ __forceinline__ v4i hi4(const uint32_t *q) {
+    return vec((q[0] >> 4) & LO4, (q[1] >> 4) & LO4, (q[2] >> 4) & LO4, (q[3] >> 4) & LO4);
+}
+
+// ------------------------------------------------------------- Q4_K
+// 144 bytes: d, dmin, 12 bytes of 6-bit scales/minimums, 128 bytes of
+// nibbles (dtype.rs:441-457): byte 16 + 32c + l holds element 64c + l (low
+// nibble) and 64c + 32 + l (high).  Lane group g takes c = g: its sub-blocks
+// are 2g (steps 0, 1) and 2g + 1 (steps 2, 3).
+__device__ __forceinline__ void k_scale_min(const uint32_t (&h)[4], int j, float &s, float &m) {
+    // kapel-cpu/src/quantized.rs:603-616 (k_scales), j = 0..7.
+    uint32_t sc, mn;
+    int jj = j & 3;
+    if (j < 4) {
+        sc = byte_of(h[1], jj) & 63u;
+        mn = byte_of(h[2], jj) & 63u;
+    } else {
+        sc = (byte_of(h[3], jj) & 15u) | ((byte_of(h[1], jj) >> 6) << 4);
+        mn = (byte_of(h[3], jj) >> 4) | ((byte_of(h[2], jj) >> 6) << 4);
+    }
+    s = f16(h[0] & 0xffffu) * (float)sc;
+    m = f16(h[0] >> 16) * (float)mn;
+}
+
+struct Q4K {
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 144;
+    struct Regs {
+        uint32_t h[4], q[8];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)u * BYTES;
+        ldw<4>(r.h, b);
+        ldw<8>(r.q, b + 16 + 32 * g);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        const uint32_t *q = r.q + 4 * (s & 1);
+        return (s >> 1) ? hi4(q) : lo4(q);
+    }
+    __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
+        k_scale_min(r.h, 2 * g + (s >> 1), sc, mn);
+    }
+};
+
+// ------------------------------------------------------------- Q5_K
+// 176 bytes: as Q4_K with 32 bytes of fifth bits at 16: bit j of byte l is
+// the fifth bit of element 32j + l; nibbles at 48.
+struct Q5K {
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 176;
+    struct Regs {
+        uint32_t h[4], qh[8], q[8];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)u * BYTES;
+        ldw<4>(r.h, b);
+        ldw<8>(r.qh, b + 16);
+        ldw<8>(r.q, b + 48 + 32 * g);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int g) {
+        const uint32_t *q = r.q + 4 * (s & 1), *h = r.qh + 4 * (s & 1);
+        int j = 2 * g + (s >> 1);
+        v4i c = (s >> 1) ? hi4(q) : lo4(q);
+        for (int i = 0; i < 4; i++) c[i] |= (int)(((h[i] >> j) & 0x01010101u) << 4);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
+        k_scale_min(r.h, 2 * g + (s >> 1), sc, mn);
+    }
+};
+
+// ------------------------------------------------------------- Q6_K
+// 210 bytes (dtype.rs:458-469): 128 bytes of low nibbles, 64 of 2-bit
+// highs, 16 signed scales, d.  Element 128h + 32t + l: low nibble t / 2 of
+// byte 64h + 32(t % 2) + l, high bits 2t of byte 128 + 32h + l, scale
+// (128h + 32t + l) / 16.  Lane group g: h = g / 2, t % 2 = g % 2; step s:
+// t = g % 2 + 2(s / 2), l = 16(s % 2) .. + 15.  Codes are stored + 32.
+struct Q6K {
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 210;
+    struct Regs {
+        uint32_t ql[8], qh[8], sc[2], d;
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)u * BYTES;
+        int h = g >> 1, q = g & 1;
+        run<32>(r.ql, b + 64 * h + 32 * q);
+        run<32>(r.qh, b + 128 + 32 * h);
+        run<8>(r.sc, b + 192 + 8 * h);
+        r.d = ld16(b + 208);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int g) {
+        const uint32_t *l = r.ql + 4 * (s & 1), *h = r.qh + 4 * (s & 1);
+        int ls = 4 * (s >> 1), hs = 2 * (g & 1) + 4 * (s >> 1);
+        v4i c;
+        for (int i = 0; i < 4; i++)
+            c[i] = (int)(((l[i] >> ls) & LO4) | (((h[i] >> hs) & 0x03030303u) << 4));
+        return c;
+    }
+    __device__ static int xpos(int g, int s) {
+        return 128 * (g >> 1) + 32 * ((g & 1) + 2 * (s >> 1)) + 16 * (s & 1);
+    }
+    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
+        int i = 2 * (g & 1) + 4 * (s >> 1) + (s & 1);  // byte of the 8 loaded
+        sc = f16(r.d) * (float)(int8_t)byte_of(r.sc[i >> 2], i & 3);
+        mn = 32.0f * sc;
+    }
+    static constexpr int SIGNED_OFFSET = 32;
+};
+
+// ------------------------------------------------------------- Q2_K
+// 84 bytes (dtype.rs:413-422): 16 scale bytes (low nibble scale, high
+// minimum), 64 bytes of 2-bit codes, d, dmin.  Element 128h + 32t + l: bits
+// 2t of byte 16 + 32h + l; group e / 16.  Lane group g: h = g / 2, l =
+// 16(g % 2) .. + 15; step s: t = s.
+struct Q2K {
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 84;
+    struct Regs {
+        uint32_t q[4], sc[2], dd;
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)u * BYTES;
+        int h = g >> 1;
+        ldw<4>(r.q, b + 16 + 32 * h + 16 * (g & 1));
+        ldw<2>(r.sc, b + 8 * h);
+        r.dd = ld32(b + 80);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        v4i c;
+        for (int i = 0; i < 4; i++) c[i] = (int)((r.q[i] >> (2 * s)) & 0x03030303u);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 128 * (g >> 1) + 32 * s + 16 * (g & 1); }
+    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
+        int i = 2 * s + (g & 1);
+        uint32_t k = byte_of(r.sc[i >> 2], i & 3);
+        sc = f16(r.dd & 0xffffu) * (float)(k & 15u);
+        mn = f16(r.dd >> 16) * (float)(k >> 4);
+    }
+};
+
+// ------------------------------------------------------------- Q3_K
+// 110 bytes (dtype.rs:423-440): 32 bytes of high-bit masks, 64 of 2-bit
+// codes, 12 of packed 6-bit scales, d.  Element 128h + 32t + l: low bits 2t
+// of byte 32 + 32h + l, high bit 4h + t of byte l; value d scale ((low |
+// high << 2) - 4).  Lanes as Q2_K.
+struct Q3K {
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 110;
+    struct Regs {
+        uint32_t hm[4], q[4], sc[3], d;
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)u * BYTES;
+        int h = g >> 1;
+        run<16>(r.hm, b + 16 * (g & 1));
+        run<16>(r.q, b + 32 + 32 * h + 16 * (g & 1));
+        run<12>(r.sc, b + 96);
+        r.d = ld16(b + 108);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int g) {
+        int hs = 4 * (g >> 1) + s;
+        v4i c;
+        for (int i = 0; i < 4; i++)
+            c[i] = (int)(((r.q[i] >> (2 * s)) & 0x03030303u) | (((r.hm[i] >> hs) & 0x01010101u) << 2));
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return Q2K::xpos(g, s); }
+    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
+        int i = 8 * (g >> 1) + 2 * s + (g & 1);
+        int a = i % 8, c = 8 + i % 4;
+        uint32_t lo = (byte_of(r.sc[a >> 2], a & 3) >> (4 * (i / 8))) & 15u;
+        uint32_t hi = (byte_of(r.sc[c >> 2], c & 3) >> (2 * (i / 4))) & 3u;
+        sc = f16(r.d) * (float)((int)(lo | (hi << 4)) - 32);
+        mn = 4.0f * sc;
+    }
+};
+
+// ----------------------------------------------- blocks of 32 elements
+// A unit is 4 blocks: lane group g takes block 4u + g (steps 0 and 1: its
+// elements 0..15 and 16..31).  Lanes whose block lies beyond K load nothing.
+__device__ __forceinline__ void nib_codes(v4i &c, const uint32_t *q, int s) {
+    c = s ? hi4(q) : lo4(q);
+}
+
+// Q4_0: 18 bytes, d then 16 bytes (byte j: element j low, j + 16 high).
+struct Q4_0 {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 18;
+    struct Regs {
+        uint32_t w[5];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        run<18>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        uint32_t q[4];
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+        v4i c;
+        nib_codes(c, q, s);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = f16(r.w[0] & 0xffffu);
+        mn = 8.0f * sc;
+    }
+};
+
+// Q4_1: 20 bytes, d, m, then nibbles; w = d q + m.
+struct Q4_1 {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 20;
+    struct Regs {
+        uint32_t w[5];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        ldw<5>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        v4i c;
+        nib_codes(c, r.w + 1, s);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = f16(r.w[0] & 0xffffu);
+        mn = -f16(r.w[0] >> 16);
+    }
+};
+
+// Fifth bits of Q5_0 / Q5_1: bits j .. j + 3 of `high` to bit 4 of bytes.
+__device__ __forceinline__ uint32_t spread4(uint32_t high, int j) {
+    uint32_t x = (high >> j) & 15u;
+    return ((x * 0x00204081u) & 0x01010101u) << 4;
+}
+
+// Q5_0: 22 bytes, d, 4 bytes of fifth bits (bit j: element j), nibbles;
+// w = d (q - 16).  Q5_1: 24 bytes, d, m, fifth bits, nibbles; w = d q + m.
+template <bool ONE>
+struct Q5x {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = ONE ? 24 : 22;
+    struct Regs {
+        uint32_t w[(BYTES + 3) / 4];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        const uint8_t *b = row + (size_t)(4 * u + g) * BYTES;
+        if (ONE) ldw<6>(*reinterpret_cast<uint32_t(*)[6]>(r.w), b);
+        else run<22>(*reinterpret_cast<uint32_t(*)[6]>(r.w), b);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        uint32_t high, q[4];
+        if (ONE) {
+            high = r.w[1];
+            for (int i = 0; i < 4; i++) q[i] = r.w[2 + i];
+        } else {
+            high = __builtin_amdgcn_alignbyte(r.w[1], r.w[0], 2);
+            for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(r.w[2 + i], r.w[1 + i], 2);
+        }
+        v4i c;
+        nib_codes(c, q, s);
+        for (int i = 0; i < 4; i++) c[i] |= (int)spread4(high, 16 * s + 4 * i);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = f16(r.w[0] & 0xffffu);
+        mn = ONE ? -f16(r.w[0] >> 16) : 16.0f * sc;
+    }
+};
+using Q5_0 = Q5x<false>;
+using Q5_1 = Q5x<true>;
+
+// Q8_0: 34 bytes, d then 32 signed bytes (dtype.rs:375-378).
+struct Q8_0 {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 34;
+    struct Regs {
+        uint32_t w[9];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        run<34>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        v4i c;
+        for (int i = 0; i < 4; i++)
+            c[i] = (int)__builtin_amdgcn_alignbyte(r.w[4 * s + i + 1], r.w[4 * s + i], 2);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = f16(r.w[0] & 0xffffu);
+        mn = 0.0f;
+    }
+};
+
+// Kapel int8 / int4 in groups of G (a multiple of 32): an f32 scale, then G
+// bytes, or G / 2 bytes of nibbles (element 2i low, 2i + 1 high)
+// (dtype.rs:364-374).  Lane group g takes the 32 elements of piece 4u + g.
+template <int G>
+struct Int8G {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G;
+    struct Regs {
+        uint32_t scale, q[8];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        int p = 4 * u + g;
+        const uint8_t *b = row + (size_t)(32 * p / G) * BYTES;
+        r.scale = ld32(b);
+        ldw<8>(r.q, b + 4 + (32 * p) % G);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        return vec(r.q[4 * s], r.q[4 * s + 1], r.q[4 * s + 2], r.q[4 * s + 3]);
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = __uint_as_float(r.scale);
+        mn = 0.0f;
+    }
+};
+
+template <int G>
+struct Int4G {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G / 2;
+    struct Regs {
+        uint32_t scale, q[4];
+    };
+    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+        int p = 4 * u + g;
+        const uint8_t *b = row + (size_t)(32 * p / G) * BYTES;
+        r.scale = ld32(b);
+        ldw<4>(r.q, b + 4 + ((32 * p) % G) / 2);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        v4i c;
+        for (int i = 0; i < 2; i++) {
+            uint32_t w = r.q[2 * s + i], lo = w & LO4, hi = (w >> 4) & LO4;
+            c[2 * i] = (int)__builtin_amdgcn_perm(hi, lo, 0x05010400u);
+            c[2 * i + 1] = (int)__builtin_amdgcn_perm(hi, lo, 0x07030602u);
+        }
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
+        sc = __uint_as_float(r.scale);
+        mn = 8.0f * sc;
+    }
+};
+
+}  // namespace lanes
+}  // namespace kh

@@ -10,7 +10,7 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 CSRC = os.path.join(ROOT, "kapel_amd", "csrc")
 OUT = os.path.join(HERE, "libkapel_hip_emu.so")
 CLANG = os.environ.get("EMU_CXX", "/opt/rocm/lib/llvm/bin/clang++")
-SOURCES = ["kh_kernels.hip", "kh_api.cpp", "kh_quantize.cpp"]
+SOURCES = ["kh_kernels.hip", "kh_gemv.hip", "kh_api.cpp", "kh_quantize.cpp"]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer", "-fPIC",
          "-ffp-contract=off", "-I", HERE, "-pthread", "-Wno-unused-command-line-argument"]
 

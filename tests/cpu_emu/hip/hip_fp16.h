@@ -13,3 +13,13 @@ inline __half __float2half_rn(float v) {
     return out;
 }
 inline uint16_t __half_as_ushort(__half h) { return h.bits; }
+inline __half __ushort_as_half(uint16_t bits) {
+    __half out;
+    out.bits = bits;
+    return out;
+}
+inline float __half2float(__half h) {
+    _Float16 v;
+    std::memcpy(&v, &h.bits, 2);
+    return (float)v;
+}

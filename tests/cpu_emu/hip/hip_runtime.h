@@ -42,6 +42,9 @@ struct int2 {
 struct uint2 {
     unsigned x, y;
 };
+struct float4 {
+    float x, y, z, w;
+};
 
 namespace emu {
 
@@ -119,6 +122,12 @@ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     return out;
 }
 
+// v_alignbyte_b32: bits 8 (s % 4) .. 8 (s % 4) + 31 of {hi:lo}.
+inline uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t s) {
+    uint64_t both = ((uint64_t)hi << 32) | lo;
+    return (uint32_t)(both >> (8 * (s & 3)));
+}
+
 template <class T>
 T atomic_load(const T *p) {
     T v;
@@ -142,6 +151,7 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define __shfl_xor(v, m, ...) emu::shfl_xor((v), (m) __VA_OPT__(, ) __VA_ARGS__)
 #define __builtin_amdgcn_mfma_i32_16x16x64_i8(...) emu::mfma_i8(__VA_ARGS__)
 #define __builtin_amdgcn_perm(hi, lo, s) emu::perm((hi), (lo), (s))
+#define __builtin_amdgcn_alignbyte(hi, lo, s) emu::alignbyte((hi), (lo), (s))
 #define __hip_atomic_fetch_add(p, v, order, scope) __atomic_fetch_add((p), (v), __ATOMIC_SEQ_CST)
 #define __hip_atomic_load(p, order, scope) emu::atomic_load(p)
 #define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)

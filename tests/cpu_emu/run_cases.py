@@ -208,8 +208,12 @@ def main(which):
     case_product(Q8_0, 0, 5, 96, 2)        # K % 64 == 32: a step of one block
     case_product(Q4K, 0, 100, 2048, 2)      # several tiles and workgroups
     case_product(Q6K, 0, 33, 1024, 3)
+    case_product(Q4K, 0, 100, 2048, 8)      # K in two chunks of the small-M product
+    case_product(Q4_0, 0, 40, 4096, 5)      # four chunks, two waves per tile
+    case_product(Q3K, 0, 20, 2048, 7)
     for fmt, group in BYTE_FORMATS:
         case_bytes(fmt, group, 13, 1024, 1 if which == "quick" else 6)
+    case_bytes(Q6K, 0, 40, 4096, 16)        # byte activations, 16 rows, four chunks
     if which == "all":
         for fmt, group in FORMATS:
             for rows in (3, 17):
