@@ -33,6 +33,9 @@ def build(verbose=False):
     units = (
         ("kh_kernels.hip", HIPCC, HIP_FLAGS),
         ("kh_gemv.hip", HIPCC, HIP_FLAGS),
+        ("kh_gemv_k.hip", HIPCC, HIP_FLAGS),
+        ("kh_gemv_b.hip", HIPCC, HIP_FLAGS),
+        ("kh_gemv_i.hip", HIPCC, HIP_FLAGS),
         ("kh_api.cpp", HIPCC, HIP_FLAGS),
         ("kh_quantize.cpp", "g++", HOST_FLAGS),
     )

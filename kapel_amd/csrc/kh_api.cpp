@@ -96,21 +96,27 @@ Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
 // The small-M product: activation rows it takes in one launch.
 int gemv_max_rows(int planes) { return planes == 1 ? 16 : 8; }
 
-// Its split: tiles per workgroup (4, 2 or 1; as many as leave a workgroup
-// for each of the 256 CUs), waves per tile (4 / tiles) splitting K, and
-// chunks of K of at most 8192 activations (rows x chunk) prepared at a time.
-// A function of the shapes only.
+// Its split, a function of the shapes only: tiles per workgroup (4, 2 or 1:
+// as many as still leave a workgroup for each of the 256 CUs), waves per tile
+// (up to 16 or 8 waves a workgroup, not more than the units of K) splitting K, and
+// chunks of K whose activations fit the preparation (16 per thread) and LDS.
 struct GemvSplit {
     int units, chunk, tiles, kw;
 };
 
-GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows) {
+GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes) {
     GemvSplit g{};
     g.units = (int)div_up(k, unit);
     g.tiles = 4;
     while (g.tiles > 1 && div_up(tiles, g.tiles) < 256) g.tiles /= 2;
-    g.kw = 4 / g.tiles;
-    g.chunk = std::max(1, std::min(g.units, 8192 / (rows * unit)));
+    g.kw = std::max(1, std::min(gemv_max_waves(planes, rows) / g.tiles, g.units));
+    if (getenv("KH_TUNE_KW")) g.kw = std::max(1, std::min(atoi(getenv("KH_TUNE_KW")), gemv_max_waves(planes, rows) / g.tiles));
+    int threads = 64 * g.tiles * g.kw;
+    int by_threads = 16 * threads / (rows * unit);
+    // LDS: 16 + span (rows planes + 1 + rows / 2) + waves 64 rows <= 64 KiB.
+    long room = 65536 - 16 - 64L * g.tiles * g.kw * rows;
+    int by_lds = (int)(room / ((long)unit * rows * planes + unit + (long)unit * rows / 2));
+    g.chunk = std::max(1, std::min({g.units, by_threads, by_lds}));
     return g;
 }
 
@@ -118,7 +124,7 @@ GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows) {
 // prepared activations, then the partial sums.
 struct Layout {
     uint64_t kpad;
-    uint64_t counters_off, planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off;
+    uint64_t counters_off, planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off, xcopy_off;
     uint64_t partials_off, total;
 };
 
@@ -138,6 +144,10 @@ Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats) {
     at = align_up(at + rows * (k / 16) * 4, 256);
     l.xsumi16_off = at;
     at = align_up(at + rows * (k / 16) * 4, 256);
+    // A copy of x for the small-M product when x is not aligned for its
+    // vector loads.
+    l.xcopy_off = at;
+    if (rows <= 16) at = align_up(at + rows * k * 4, 256);
     l.partials_off = at;
     // Partial sums of the largest launch: segments x rows x columns.
     at = align_up(at + partial_floats * 4, 256);
@@ -187,11 +197,14 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         if (L.tiles == 0) continue;
         int steps = (int)div_up(k, 64);
         int unit = gemv_unit(w.format, w.group);
-        if (unit && rows <= (uint64_t)gemv_max_rows(planes)) {
+        // The small-M product reads each matrix at 32-bit offsets.
+        bool offsets32 = true;
+        for (uint32_t m : L.members) offsets32 = offsets32 && weights[m].bytes < (1ull << 31);
+        if (unit && offsets32 && rows <= (uint64_t)gemv_max_rows(planes)) {
             L.gemv = true;
             L.r0 = 0;
             L.rows = (int)rows;
-            L.gsplit = gemv_split(k, unit, L.tiles, L.rows);
+            L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes);
             fn(L);
             continue;
         }
@@ -304,6 +317,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             for (int m = 0; m < a.count; m++) {
                 const kh_weight &wm = weights[L.members[m]];
                 a.w[m] = static_cast<const uint8_t *>(wm.data);
+                a.wbytes[m] = (uint32_t)wm.bytes;
                 a.n[m] = wm.n;
                 a.col0[m] = col0[L.members[m]];
                 a.tile0[m] = tiles;
@@ -316,11 +330,21 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.chunk = L.gsplit.chunk;
             a.total_tiles = tiles;
             a.tiles = L.gsplit.tiles;
+            a.tiles_log2 = a.tiles == 4 ? 2 : a.tiles == 2 ? 1 : 0;
             a.kw = L.gsplit.kw;
             a.rows = L.rows;
             a.x_kind = x_kind;
             a.x = x;
-            a.x_vec = ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) == 0;
+            if ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) {
+                void *copy = ws + l.xcopy_off;
+                hipError_t e = hipMemcpyAsync(copy, x, rows * k * kind_bytes(x_kind),
+                                              hipMemcpyDeviceToDevice, s);
+                if (e != hipSuccess) {
+                    err = e;
+                    return;
+                }
+                a.x = copy;
+            }
             a.out_kind = out_kind;
             a.out = out;
             a.out_stride = c.width;
@@ -494,25 +518,26 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
     const kh_weight &w = *weight;
     int unit = gemv_unit(w.format, w.group);
-    if (unit && rows <= (uint64_t)gemv_max_rows(1)) {
+    if (unit && rows <= (uint64_t)gemv_max_rows(1) && (uintptr_t)q % 4 == 0 && w.bytes < (1ull << 31)) {
         // The bytes go through the small-M product's own preparation.
         GemvArgs g{};
         g.count = 1;
         g.w[0] = static_cast<const uint8_t *>(w.data);
+        g.wbytes[0] = (uint32_t)w.bytes;
         g.n[0] = w.n;
         uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
         g.row_bytes = k / len * size;
         g.k = (int)k;
-        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), (int)rows);
+        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), (int)rows, 1);
         g.units = sp.units;
         g.chunk = sp.chunk;
         g.total_tiles = (int)div_up(w.n, 16);
         g.tiles = sp.tiles;
+        g.tiles_log2 = g.tiles == 4 ? 2 : g.tiles == 2 ? 1 : 0;
         g.kw = sp.kw;
         g.rows = (int)rows;
         g.x_kind = KH_I8_INTERNAL;
         g.x = q;
-        g.x_vec = 0;
         g.dots = dots;
         g.width = w.n;
         return launch_gemv(w.format, w.group, 1, g, s) == hipSuccess ? KH_OK : KH_ERR_HIP;

@@ -80,16 +80,16 @@ struct QmvArgs {
 struct GemvArgs {
     int count;
     const uint8_t *w[MAX_WEIGHTS];
+    uint32_t wbytes[MAX_WEIGHTS];  // bytes of each matrix (< 2 GiB)
     uint64_t n[MAX_WEIGHTS];
     uint64_t col0[MAX_WEIGHTS];
     int tile0[MAX_WEIGHTS];
     uint64_t row_bytes;
     int k, units, chunk;
-    int total_tiles, tiles, kw;
+    int total_tiles, tiles, tiles_log2, kw;  // tiles: 1, 2 or 4
     int rows;                     // activation rows
     uint32_t x_kind;
-    const void *x;                // [rows, k]
-    int x_vec;                    // x may be read 4 elements at a time
+    const void *x;                // [rows, k], aligned to 4 elements
     uint32_t out_kind;
     void *out;                    // [rows, out_stride]
     uint64_t out_stride;
@@ -124,6 +124,8 @@ hipError_t launch_qmv(uint32_t fmt, uint32_t group, int planes, const QmvArgs &a
                       size_t lds, hipStream_t s);
 // Units of the small-M product for a format (0: not read by it).
 int gemv_unit(uint32_t fmt, uint32_t group);
+// Waves of one of its workgroups at most.
+int gemv_max_waves(int planes, int rows);
 // Bytes of LDS of one of its workgroups.
 size_t gemv_lds(int rows, int planes, int chunk, int unit, int waves);
 hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s);

@@ -10,10 +10,10 @@
 // unit offset xpos(g, s), consecutive.  Each lane therefore gets back in C
 // exactly the dots of its own groups and applies their scales itself.
 //
-// A reader loads its lane's bytes with the widest loads the alignment allows
-// (16-byte loads at 4-byte-aligned addresses; formats whose blocks start at
-// even addresses only are read from the 4-byte-aligned address below and put
-// back in place with v_alignbyte), never touching a byte outside the unit.
+// A reader loads its lane's bytes with the widest buffer loads the alignment
+// allows (16-byte loads at 4-byte-aligned offsets; formats whose blocks start
+// at even offsets only are read from the 4-byte-aligned offset below and put
+// back in place with v_alignbyte).
 // Scales and minimums are the f32 products of the CPU decoders
 // (kapel-cpu/src/quantized.rs:403-682, k_scales :603-616); element layouts
 // follow kapel-core/src/dtype.rs:342-520.
@@ -29,41 +29,60 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 constexpr uint32_t LO4 = 0x0f0f0f0fu;
 
 // ---------------------------------------------------------------- loads
-__device__ __forceinline__ uint32_t ld32(const uint8_t *p) {  // p % 4 == 0
-    return *reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
-}
-__device__ __forceinline__ uint32_t ld16(const uint8_t *p) {  // p % 2 == 0
-    return *reinterpret_cast<const uint16_t *>(__builtin_assume_aligned(p, 2));
-}
-// N dwords at a 4-byte-aligned address (merged into 16-byte loads).
-template <int N>
-__device__ __forceinline__ void ldw(uint32_t (&v)[N], const uint8_t *p) {
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(p, 4));
-#pragma unroll
-    for (int i = 0; i < N; i++) v[i] = q[i];
+// A weight matrix is read through a buffer resource: raw buffer loads at
+// 32-bit byte offsets, bounds-checked by the hardware against the matrix
+// size rounded up to whole dwords.  An offset past the end reads zeros and
+// touches no memory, which lets a lane with nothing to read still issue its
+// loads (NONE), so every wave issues the same loads in the same order.
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x3 __attribute__((ext_vector_type(3)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+constexpr uint32_t NONE = 0x80000000u;  // past every matrix (< 2 GiB each)
+
+struct Src {
+    __amdgpu_buffer_rsrc_t r;
+};
+
+__device__ __forceinline__ Src source(const void *base, uint32_t bytes) {
+    return Src{__builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)((bytes + 3u) & ~3u),
+                                                 0x00020000)};
 }
 
-// The bytes [p, p + R) of an even address p, as ceil(R / 4) dwords in
-// place.  Loads from p - (p % 4): the two bytes below p belong to the
-// tensor (a tensor starts at a multiple of 4), and nothing at or beyond
-// p + R is read.
+// N dwords at byte offset off (a multiple of 4, or NONE).
+template <int N>
+__device__ __forceinline__ void ldb(uint32_t (&v)[N], const Src &s, uint32_t off) {
+    int i = 0;
+#pragma unroll
+    for (; i + 4 <= N; i += 4) {
+        u32x4 t = __builtin_amdgcn_raw_buffer_load_b128(s.r, (int)(off + 4 * i), 0, 0);
+        v[i] = t.x, v[i + 1] = t.y, v[i + 2] = t.z, v[i + 3] = t.w;
+    }
+    if (N - i == 3) {
+        u32x3 t = __builtin_amdgcn_raw_buffer_load_b96(s.r, (int)(off + 4 * i), 0, 0);
+        v[i] = t.x, v[i + 1] = t.y, v[i + 2] = t.z;
+    } else if (N - i == 2) {
+        u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(s.r, (int)(off + 4 * i), 0, 0);
+        v[i] = t.x, v[i + 1] = t.y;
+    } else if (N - i == 1) {
+        v[i] = __builtin_amdgcn_raw_buffer_load_b32(s.r, (int)(off + 4 * i), 0, 0);
+    }
+}
+
+// The bytes [off, off + R) at an even offset, as ceil(R / 4) dwords in
+// place: the dwords from off - (off % 4) on, then shifted by v_alignbyte.
+// The two bytes below an odd-halfword offset belong to the matrix (which
+// starts at a multiple of 4); the bytes past the run are in the matrix's
+// last dword or beyond it (zeros).
 template <int R>
-__device__ __forceinline__ void run(uint32_t (&w)[(R + 3) / 4], const uint8_t *p) {
+__device__ __forceinline__ void run(uint32_t (&w)[(R + 3) / 4], const Src &src, uint32_t off) {
     static_assert(R % 2 == 0, "even runs only");
-    constexpr int F = R / 4, W = (R + 3) / 4;
-    const uint32_t s = (uint32_t)(uintptr_t)p & 2u;
-    const uint8_t *a = p - s;
-    uint32_t v[F + 2];
-    const uint32_t *q = reinterpret_cast<const uint32_t *>(__builtin_assume_aligned(a, 4));
+    constexpr int D = (R + 5) / 4, W = (R + 3) / 4;
+    const uint32_t s = off & 2u;
+    uint32_t v[D + 1];
+    ldb<D>(*reinterpret_cast<uint32_t(*)[D]>(v), src, off - s);
+    v[D] = 0u;
 #pragma unroll
-    for (int i = 0; i < F; i++) v[i] = q[i];
-    if (R % 4 == 2) v[F] = s ? q[F] : ld16(a + 4 * F);
-    else v[F] = s ? ld16(a + 4 * F) : 0u;
-    v[F + 1] = 0u;
-#pragma unroll
-    for (int i = 0; i < W; i++) v[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], s);
-#pragma unroll
-    for (int i = 0; i < W; i++) w[i] = v[i];
+    for (int i = 0; i < W; i++) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], s);
 }
 
 __device__ __forceinline__ float f16(uint32_t h) { return __half2float(__ushort_as_half((uint16_t)h)); }
@@ -84,19 +103,25 @@ __device__ __forceinline__ v4i hi4(const uint32_t *q) {
 // nibbles (dtype.rs:441-457): byte 16 + 32c + l holds element 64c + l (low
 // nibble) and 64c + 32 + l (high).  Lane group g takes c = g: its sub-blocks
 // are 2g (steps 0, 1) and 2g + 1 (steps 2, 3).
-__device__ __forceinline__ void k_scale_min(const uint32_t (&h)[4], int j, float &s, float &m) {
-    // kapel-cpu/src/quantized.rs:603-616 (k_scales), j = 0..7.
+// The scales and minimums of sub-blocks 2g and 2g + 1 at once: bytes 2g,
+// 2g + 1 of the 6-bit fields (k_scales, quantized.rs:603-616), two lanes of
+// 16 bits each, then each byte to f32.
+__device__ __forceinline__ void k_pair(const uint32_t (&h)[4], int g, float (&s)[2], float (&m)[2]) {
+    const int sh = 16 * (g & 1);
     uint32_t sc, mn;
-    int jj = j & 3;
-    if (j < 4) {
-        sc = byte_of(h[1], jj) & 63u;
-        mn = byte_of(h[2], jj) & 63u;
+    if (g < 2) {
+        sc = (h[1] >> sh) & 0x3f3fu;
+        mn = (h[2] >> sh) & 0x3f3fu;
     } else {
-        sc = (byte_of(h[3], jj) & 15u) | ((byte_of(h[1], jj) >> 6) << 4);
-        mn = (byte_of(h[3], jj) >> 4) | ((byte_of(h[2], jj) >> 6) << 4);
+        uint32_t lo = h[3] >> sh;
+        sc = (lo & 0x0f0fu) | ((h[1] >> (sh + 2)) & 0x3030u);
+        mn = ((lo >> 4) & 0x0f0fu) | ((h[2] >> (sh + 2)) & 0x3030u);
     }
-    s = f16(h[0] & 0xffffu) * (float)sc;
-    m = f16(h[0] >> 16) * (float)mn;
+    const float d = f16(h[0] & 0xffffu), dmin = f16(h[0] >> 16);
+    s[0] = d * (float)(sc & 0xffu);
+    s[1] = d * (float)(sc >> 8);
+    m[0] = dmin * (float)(mn & 0xffu);
+    m[1] = dmin * (float)(mn >> 8);
 }
 
 struct Q4K {
@@ -104,18 +129,18 @@ struct Q4K {
     struct Regs {
         uint32_t h[4], q[8];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)u * BYTES;
-        ldw<4>(r.h, b);
-        ldw<8>(r.q, b + 16 + 32 * g);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
+        ldb<4>(r.h, src, b);
+        ldb<8>(r.q, src, b + 16 + 32 * g);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         const uint32_t *q = r.q + 4 * (s & 1);
         return (s >> 1) ? hi4(q) : lo4(q);
     }
     __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
-        k_scale_min(r.h, 2 * g + (s >> 1), sc, mn);
+    __device__ static void scales(const Regs &r, int g, float (&sc)[2], float (&mn)[2]) {
+        k_pair(r.h, g, sc, mn);
     }
 };
 
@@ -127,11 +152,11 @@ struct Q5K {
     struct Regs {
         uint32_t h[4], qh[8], q[8];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)u * BYTES;
-        ldw<4>(r.h, b);
-        ldw<8>(r.qh, b + 16);
-        ldw<8>(r.q, b + 48 + 32 * g);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
+        ldb<4>(r.h, src, b);
+        ldb<8>(r.qh, src, b + 16);
+        ldb<8>(r.q, src, b + 48 + 32 * g);
     }
     __device__ static v4i codes(const Regs &r, int s, int g) {
         const uint32_t *q = r.q + 4 * (s & 1), *h = r.qh + 4 * (s & 1);
@@ -141,8 +166,8 @@ struct Q5K {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
-        k_scale_min(r.h, 2 * g + (s >> 1), sc, mn);
+    __device__ static void scales(const Regs &r, int g, float (&sc)[2], float (&mn)[2]) {
+        k_pair(r.h, g, sc, mn);
     }
 };
 
@@ -157,13 +182,15 @@ struct Q6K {
     struct Regs {
         uint32_t ql[8], qh[8], sc[2], d;
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)u * BYTES;
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
         int h = g >> 1, q = g & 1;
-        run<32>(r.ql, b + 64 * h + 32 * q);
-        run<32>(r.qh, b + 128 + 32 * h);
-        run<8>(r.sc, b + 192 + 8 * h);
-        r.d = ld16(b + 208);
+        run<32>(r.ql, src, b + 64 * h + 32 * q);
+        run<32>(r.qh, src, b + 128 + 32 * h);
+        run<8>(r.sc, src, b + 192 + 8 * h);
+        uint32_t d[1];
+        run<2>(d, src, b + 208);
+        r.d = d[0] & 0xffffu;
     }
     __device__ static v4i codes(const Regs &r, int s, int g) {
         const uint32_t *l = r.ql + 4 * (s & 1), *h = r.qh + 4 * (s & 1);
@@ -176,10 +203,13 @@ struct Q6K {
     __device__ static int xpos(int g, int s) {
         return 128 * (g >> 1) + 32 * ((g & 1) + 2 * (s >> 1)) + 16 * (s & 1);
     }
-    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
-        int i = 2 * (g & 1) + 4 * (s >> 1) + (s & 1);  // byte of the 8 loaded
-        sc = f16(r.d) * (float)(int8_t)byte_of(r.sc[i >> 2], i & 3);
-        mn = 32.0f * sc;
+    __device__ static void scales(const Regs &r, int g, float (&sc)[4], float (&mn)[4]) {
+        const float d = f16(r.d);
+        for (int s = 0; s < 4; s++) {
+            int i = 2 * (g & 1) + 4 * (s >> 1) + (s & 1);  // byte of the 8 loaded
+            sc[s] = d * (float)(int8_t)byte_of(r.sc[i >> 2], i & 3);
+            mn[s] = 32.0f * sc[s];
+        }
     }
     static constexpr int SIGNED_OFFSET = 32;
 };
@@ -194,12 +224,14 @@ struct Q2K {
     struct Regs {
         uint32_t q[4], sc[2], dd;
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)u * BYTES;
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
         int h = g >> 1;
-        ldw<4>(r.q, b + 16 + 32 * h + 16 * (g & 1));
-        ldw<2>(r.sc, b + 8 * h);
-        r.dd = ld32(b + 80);
+        ldb<4>(r.q, src, b + 16 + 32 * h + 16 * (g & 1));
+        ldb<2>(r.sc, src, b + 8 * h);
+        uint32_t dd[1];
+        ldb<1>(dd, src, b + 80);
+        r.dd = dd[0];
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         v4i c;
@@ -207,11 +239,14 @@ struct Q2K {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 128 * (g >> 1) + 32 * s + 16 * (g & 1); }
-    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
-        int i = 2 * s + (g & 1);
-        uint32_t k = byte_of(r.sc[i >> 2], i & 3);
-        sc = f16(r.dd & 0xffffu) * (float)(k & 15u);
-        mn = f16(r.dd >> 16) * (float)(k >> 4);
+    __device__ static void scales(const Regs &r, int g, float (&sc)[4], float (&mn)[4]) {
+        const float d = f16(r.dd & 0xffffu), dmin = f16(r.dd >> 16);
+        for (int s = 0; s < 4; s++) {
+            int i = 2 * s + (g & 1);
+            uint32_t k = byte_of(r.sc[i >> 2], i & 3);
+            sc[s] = d * (float)(k & 15u);
+            mn[s] = dmin * (float)(k >> 4);
+        }
     }
 };
 
@@ -225,13 +260,15 @@ struct Q3K {
     struct Regs {
         uint32_t hm[4], q[4], sc[3], d;
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)u * BYTES;
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
         int h = g >> 1;
-        run<16>(r.hm, b + 16 * (g & 1));
-        run<16>(r.q, b + 32 + 32 * h + 16 * (g & 1));
-        run<12>(r.sc, b + 96);
-        r.d = ld16(b + 108);
+        run<16>(r.hm, src, b + 16 * (g & 1));
+        run<16>(r.q, src, b + 32 + 32 * h + 16 * (g & 1));
+        run<12>(r.sc, src, b + 96);
+        uint32_t d[1];
+        run<2>(d, src, b + 108);
+        r.d = d[0] & 0xffffu;
     }
     __device__ static v4i codes(const Regs &r, int s, int g) {
         int hs = 4 * (g >> 1) + s;
@@ -241,13 +278,16 @@ struct Q3K {
         return c;
     }
     __device__ static int xpos(int g, int s) { return Q2K::xpos(g, s); }
-    __device__ static void scale(const Regs &r, int g, int s, float &sc, float &mn) {
-        int i = 8 * (g >> 1) + 2 * s + (g & 1);
-        int a = i % 8, c = 8 + i % 4;
-        uint32_t lo = (byte_of(r.sc[a >> 2], a & 3) >> (4 * (i / 8))) & 15u;
-        uint32_t hi = (byte_of(r.sc[c >> 2], c & 3) >> (2 * (i / 4))) & 3u;
-        sc = f16(r.d) * (float)((int)(lo | (hi << 4)) - 32);
-        mn = 4.0f * sc;
+    __device__ static void scales(const Regs &r, int g, float (&sc)[4], float (&mn)[4]) {
+        const float d = f16(r.d);
+        for (int s = 0; s < 4; s++) {
+            int i = 8 * (g >> 1) + 2 * s + (g & 1);
+            int a = i % 8, c = 8 + i % 4;
+            uint32_t lo = (byte_of(r.sc[a >> 2], a & 3) >> (4 * (i / 8))) & 15u;
+            uint32_t hi = (byte_of(r.sc[c >> 2], c & 3) >> (2 * (i / 4))) & 3u;
+            sc[s] = d * (float)((int)(lo | (hi << 4)) - 32);
+            mn[s] = 4.0f * sc[s];
+        }
     }
 };
 
@@ -264,8 +304,8 @@ struct Q4_0 {
     struct Regs {
         uint32_t w[5];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        run<18>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        run<18>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         uint32_t q[4];
@@ -275,9 +315,9 @@ struct Q4_0 {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = f16(r.w[0] & 0xffffu);
-        mn = 8.0f * sc;
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = f16(r.w[0] & 0xffffu);
+        mn[0] = 8.0f * sc[0];
     }
 };
 
@@ -287,8 +327,8 @@ struct Q4_1 {
     struct Regs {
         uint32_t w[5];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        ldw<5>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        ldb<5>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         v4i c;
@@ -296,9 +336,9 @@ struct Q4_1 {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = f16(r.w[0] & 0xffffu);
-        mn = -f16(r.w[0] >> 16);
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = f16(r.w[0] & 0xffffu);
+        mn[0] = -f16(r.w[0] >> 16);
     }
 };
 
@@ -316,10 +356,10 @@ struct Q5x {
     struct Regs {
         uint32_t w[(BYTES + 3) / 4];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        const uint8_t *b = row + (size_t)(4 * u + g) * BYTES;
-        if (ONE) ldw<6>(*reinterpret_cast<uint32_t(*)[6]>(r.w), b);
-        else run<22>(*reinterpret_cast<uint32_t(*)[6]>(r.w), b);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + (4 * u + g) * BYTES;
+        if (ONE) ldb<6>(*reinterpret_cast<uint32_t(*)[6]>(r.w), src, b);
+        else run<22>(*reinterpret_cast<uint32_t(*)[6]>(r.w), src, b);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         uint32_t high, q[4];
@@ -336,9 +376,9 @@ struct Q5x {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = f16(r.w[0] & 0xffffu);
-        mn = ONE ? -f16(r.w[0] >> 16) : 16.0f * sc;
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = f16(r.w[0] & 0xffffu);
+        mn[0] = ONE ? -f16(r.w[0] >> 16) : 16.0f * sc[0];
     }
 };
 using Q5_0 = Q5x<false>;
@@ -350,8 +390,8 @@ struct Q8_0 {
     struct Regs {
         uint32_t w[9];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
-        run<34>(r.w, row + (size_t)(4 * u + g) * BYTES);
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+        run<34>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         v4i c;
@@ -360,9 +400,9 @@ struct Q8_0 {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = f16(r.w[0] & 0xffffu);
-        mn = 0.0f;
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = f16(r.w[0] & 0xffffu);
+        mn[0] = 0.0f;
     }
 };
 
@@ -375,19 +415,21 @@ struct Int8G {
     struct Regs {
         uint32_t scale, q[8];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
         int p = 4 * u + g;
-        const uint8_t *b = row + (size_t)(32 * p / G) * BYTES;
-        r.scale = ld32(b);
-        ldw<8>(r.q, b + 4 + (32 * p) % G);
+        const uint32_t b = row + (32 * p / G) * BYTES;
+        uint32_t sc[1];
+        ldb<1>(sc, src, b);
+        r.scale = sc[0];
+        ldb<8>(r.q, src, b + 4 + (32 * p) % G);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         return vec(r.q[4 * s], r.q[4 * s + 1], r.q[4 * s + 2], r.q[4 * s + 3]);
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = __uint_as_float(r.scale);
-        mn = 0.0f;
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = __uint_as_float(r.scale);
+        mn[0] = 0.0f;
     }
 };
 
@@ -397,11 +439,13 @@ struct Int4G {
     struct Regs {
         uint32_t scale, q[4];
     };
-    __device__ static void load(Regs &r, const uint8_t *row, int u, int g) {
+    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
         int p = 4 * u + g;
-        const uint8_t *b = row + (size_t)(32 * p / G) * BYTES;
-        r.scale = ld32(b);
-        ldw<4>(r.q, b + 4 + ((32 * p) % G) / 2);
+        const uint32_t b = row + (32 * p / G) * BYTES;
+        uint32_t sc[1];
+        ldb<1>(sc, src, b);
+        r.scale = sc[0];
+        ldb<4>(r.q, src, b + 4 + ((32 * p) % G) / 2);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
         v4i c;
@@ -413,9 +457,9 @@ struct Int4G {
         return c;
     }
     __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
-    __device__ static void scale(const Regs &r, int, int, float &sc, float &mn) {
-        sc = __uint_as_float(r.scale);
-        mn = 8.0f * sc;
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = __uint_as_float(r.scale);
+        mn[0] = 8.0f * sc[0];
     }
 };
 

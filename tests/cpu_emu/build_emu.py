@@ -10,7 +10,8 @@ ROOT = os.path.dirname(os.path.dirname(HERE))
 CSRC = os.path.join(ROOT, "kapel_amd", "csrc")
 OUT = os.path.join(HERE, "libkapel_hip_emu.so")
 CLANG = os.environ.get("EMU_CXX", "/opt/rocm/lib/llvm/bin/clang++")
-SOURCES = ["kh_kernels.hip", "kh_gemv.hip", "kh_api.cpp", "kh_quantize.cpp"]
+SOURCES = ["kh_kernels.hip", "kh_gemv.hip", "kh_gemv_k.hip", "kh_gemv_b.hip", "kh_gemv_i.hip",
+           "kh_api.cpp", "kh_quantize.cpp"]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer", "-fPIC",
          "-ffp-contract=off", "-I", HERE, "-pthread", "-Wno-unused-command-line-argument"]
 
@@ -41,12 +42,15 @@ def build():
     d = digest()
     if os.path.exists(OUT) and os.path.exists(stamp) and open(stamp).read() == d:
         return OUT
-    objs = []
-    for src in SOURCES:
-        obj = os.path.join(HERE, src + ".emu.o")
-        subprocess.run([CLANG, *FLAGS, "-x", "c++", "-c", os.path.join(CSRC, src), "-o", obj],
+    objs = [os.path.join(HERE, src + ".emu.o") for src in SOURCES]
+    from concurrent.futures import ThreadPoolExecutor
+
+    def one(i):
+        subprocess.run([CLANG, *FLAGS, "-x", "c++", "-c", os.path.join(CSRC, SOURCES[i]), "-o", objs[i]],
                        check=True)
-        objs.append(obj)
+
+    with ThreadPoolExecutor(4) as pool:
+        list(pool.map(one, range(len(SOURCES))))
     subprocess.run([CLANG, "-shared", "-fsanitize=address", "-pthread", *objs, "-o", OUT], check=True)
     for obj in objs:
         os.remove(obj)

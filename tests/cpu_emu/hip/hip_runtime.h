@@ -28,6 +28,7 @@
 #define __shared__
 #define __align__(n) __attribute__((aligned(n)))
 #define __HIP_MEMORY_SCOPE_AGENT 0
+#define __HIP_MEMORY_SCOPE_WORKGROUP 1
 
 struct dim3 {
     unsigned x, y, z;
@@ -54,6 +55,7 @@ struct Lane {
     dim3 tid, bid;
 };
 inline thread_local Lane self;
+inline dim3 block_dim;
 
 struct Block {
     std::barrier<> *all = nullptr;
@@ -116,6 +118,7 @@ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
     uint32_t out = 0;
     for (int s = 0; s < 4; s++) {
         uint32_t k = (sel >> (8 * s)) & 0xff;
+        if (k == 12) continue;  // the constant 0x00
         if (k > 7) std::abort();
         out |= (uint32_t)((both >> (8 * k)) & 0xff) << (8 * s);
     }
@@ -126,6 +129,64 @@ inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
 inline uint32_t alignbyte(uint32_t hi, uint32_t lo, uint32_t s) {
     uint64_t both = ((uint64_t)hi << 32) | lo;
     return (uint32_t)(both >> (8 * (s & 3)));
+}
+
+// v_mov_b32_dpp with a quad permutation (ctrl < 0x100): lane 4i + j takes
+// lane 4i + ctrl[2j + 1 : 2j].
+inline int mov_dpp(int v, int ctrl, int, int, bool) {
+    if (ctrl >= 0x100) std::abort();
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &v, 4);
+    wave_sync();
+    int src = (l & ~3) | ((ctrl >> (2 * (l & 3))) & 3);
+    int out;
+    std::memcpy(&out, &block.slots[w][src][0], 4);
+    wave_sync();
+    return out;
+}
+
+// ds_swizzle_b32 in bit mode (offset < 0x8000): within each 32 lanes, lane l
+// takes lane ((l & and) | or) ^ xor.
+inline int ds_swizzle(int v, int offset) {
+    if (offset & 0x8000) std::abort();
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &v, 4);
+    wave_sync();
+    int am = offset & 0x1f, om = (offset >> 5) & 0x1f, xm = (offset >> 10) & 0x1f;
+    int src = (l & 32) | ((((l & 31) & am) | om) ^ xm);
+    int out;
+    std::memcpy(&out, &block.slots[w][src][0], 4);
+    wave_sync();
+    return out;
+}
+
+// Buffer resources and raw buffer loads: a dword whose offset is not
+// wholly inside num_records bytes reads as zero.
+struct BufferRsrc {
+    const uint8_t *base;
+    uint32_t num;
+};
+inline BufferRsrc make_rsrc(void *p, short, int num, int) { return BufferRsrc{(const uint8_t *)p, (uint32_t)num}; }
+inline uint32_t buf_dword(const BufferRsrc &r, int off) {
+    uint32_t o = (uint32_t)off, v = 0;
+    if ((uint64_t)o + 4 <= r.num) std::memcpy(&v, r.base + o, 4);
+    return v;
+}
+template <int N>
+struct BufVec {
+    typedef unsigned int type __attribute__((ext_vector_type(N)));
+};
+template <int N>
+inline typename BufVec<N>::type buf_load(const BufferRsrc &r, int off) {
+    typename BufVec<N>::type out;
+    for (int i = 0; i < N; i++) out[i] = buf_dword(r, off + 4 * i);
+    return out;
+}
+
+inline int frexp_exp(float v) {
+    int e = 0;
+    if (std::isfinite(v)) std::frexp(v, &e);
+    return e;
 }
 
 template <class T>
@@ -146,12 +207,25 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 
 #define threadIdx (emu::self.tid)
 #define blockIdx (emu::self.bid)
+#define blockDim (emu::block_dim)
 #define __syncthreads() (emu::block.all->arrive_and_wait())
 #define __threadfence() __atomic_thread_fence(__ATOMIC_SEQ_CST)
 #define __shfl_xor(v, m, ...) emu::shfl_xor((v), (m) __VA_OPT__(, ) __VA_ARGS__)
 #define __builtin_amdgcn_mfma_i32_16x16x64_i8(...) emu::mfma_i8(__VA_ARGS__)
 #define __builtin_amdgcn_perm(hi, lo, s) emu::perm((hi), (lo), (s))
 #define __builtin_amdgcn_alignbyte(hi, lo, s) emu::alignbyte((hi), (lo), (s))
+#define __builtin_amdgcn_mov_dpp(v, c, r, b, z) emu::mov_dpp((v), (c), (r), (b), (z))
+#define __builtin_amdgcn_ds_swizzle(v, o) emu::ds_swizzle((v), (o))
+#define __builtin_amdgcn_frexp_expf(v) emu::frexp_exp(v)
+#define __builtin_amdgcn_s_sleep(n) std::this_thread::yield()
+typedef emu::BufferRsrc __amdgpu_buffer_rsrc_t;
+#define __builtin_amdgcn_make_buffer_rsrc(p, s, n, f) emu::make_rsrc((p), (s), (n), (f))
+#define __builtin_amdgcn_raw_buffer_load_b32(r, o, so, a) emu::buf_dword((r), (o) + (so))
+#define __builtin_amdgcn_raw_buffer_load_b64(r, o, so, a) emu::buf_load<2>((r), (o) + (so))
+#define __builtin_amdgcn_raw_buffer_load_b96(r, o, so, a) emu::buf_load<3>((r), (o) + (so))
+#define __builtin_amdgcn_raw_buffer_load_b128(r, o, so, a) emu::buf_load<4>((r), (o) + (so))
+#define __builtin_amdgcn_readfirstlane(v) (v)
+#define __builtin_amdgcn_wave_barrier() emu::wave_sync()
 #define __hip_atomic_fetch_add(p, v, order, scope) __atomic_fetch_add((p), (v), __ATOMIC_SEQ_CST)
 #define __hip_atomic_load(p, order, scope) emu::atomic_load(p)
 #define __hip_atomic_store(p, v, order, scope) __atomic_store_n((p), (v), __ATOMIC_SEQ_CST)
@@ -159,6 +233,11 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
     emu::launch(kernel, dim3(grid), dim3(threads), (size_t)(lds), __VA_ARGS__)
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
+enum hipMemcpyKind { hipMemcpyDeviceToDevice = 3 };
+inline hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind, hipStream_t) {
+    std::memcpy(dst, src, n);
+    return hipSuccess;
+}
 
 inline float __uint_as_float(uint32_t u) {
     float f;
@@ -172,6 +251,8 @@ inline uint32_t __float_as_uint(float f) {
 }
 inline int min(int a, int b) { return a < b ? a : b; }
 inline int max(int a, int b) { return a > b ? a : b; }
+inline uint32_t max(uint32_t a, uint32_t b) { return a > b ? a : b; }
+inline int64_t min(int64_t a, int64_t b) { return a < b ? a : b; }
 using std::isfinite;
 
 namespace emu {
@@ -243,6 +324,7 @@ void launch(K kernel, dim3 grid, dim3 threads, size_t lds, A... args) {
     const unsigned total = grid.x * grid.y * grid.z;
     if (total == 0) return;
     fresh_block(threads.x, lds);
+    block_dim = threads;
     // Between workgroups, the last lane to arrive makes the next one's barriers.
     std::barrier<std::function<void()>> next((ptrdiff_t)threads.x,
                                              std::function<void()>([&] { fresh_block(threads.x, lds); }));

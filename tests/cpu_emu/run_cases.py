@@ -54,7 +54,12 @@ def blocks(fmt, group, count, seed):
     if fmt in (INT8, INT4):
         raw[:, :4] = np.frombuffer(rng.uniform(0.005, 0.02, count).astype(np.float32).tobytes(),
                                    dtype=np.uint8).reshape(count, 4)
-    return raw.ravel()
+    # The device reads a matrix by whole dwords: the last one may extend two
+    # bytes past an odd-halfword end, inside the same dword (never a fault on
+    # the device); the host allocation keeps those bytes addressable.
+    padded = np.zeros(count * size + 4, np.uint8)
+    padded[:count * size] = raw.ravel()
+    return padded[:count * size]
 
 
 def xs(rows, k, seed):
