@@ -93,8 +93,10 @@ Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
     return Split{segs, seg_steps, lds_bytes(rows, planes, seg_steps)};
 }
 
-// The small-M product: activation rows it takes in one launch.
+// The small-M product: activation rows of one of its workgroups, and the
+// rows it takes in one launch (in chunks of the former).
 int gemv_max_rows(int planes) { return planes == 1 ? 16 : 8; }
+constexpr uint64_t GEMV_ROWS = 64;
 
 // Its split, a function of the shapes only: tiles per workgroup (4, 2 or 1:
 // as many as still leave a workgroup for each of the 256 CUs), waves per tile
@@ -104,11 +106,11 @@ struct GemvSplit {
     int units, chunk, tiles, kw;
 };
 
-GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes) {
+GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int mchunks) {
     GemvSplit g{};
     g.units = (int)div_up(k, unit);
     g.tiles = 4;
-    while (g.tiles > 1 && div_up(tiles, g.tiles) < 256) g.tiles /= 2;
+    while (g.tiles > 1 && div_up(tiles, g.tiles) * mchunks < 256) g.tiles /= 2;
     g.kw = std::max(1, std::min(gemv_max_waves(planes, rows) / g.tiles, g.units));
     if (getenv("KH_TUNE_KW")) g.kw = std::max(1, std::min(atoi(getenv("KH_TUNE_KW")), gemv_max_waves(planes, rows) / g.tiles));
     int threads = 64 * g.tiles * g.kw;
@@ -200,11 +202,11 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         // The small-M product reads each matrix at 32-bit offsets.
         bool offsets32 = true;
         for (uint32_t m : L.members) offsets32 = offsets32 && weights[m].bytes < (1ull << 31);
-        if (unit && offsets32 && rows <= (uint64_t)gemv_max_rows(planes)) {
+        if (unit && offsets32 && rows <= GEMV_ROWS) {
             L.gemv = true;
             L.r0 = 0;
-            L.rows = (int)rows;
-            L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes);
+            L.rows = (int)std::min<uint64_t>(rows, gemv_max_rows(planes));
+            L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes, (int)div_up(rows, L.rows));
             fn(L);
             continue;
         }
@@ -333,6 +335,8 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.tiles_log2 = a.tiles == 4 ? 2 : a.tiles == 2 ? 1 : 0;
             a.kw = L.gsplit.kw;
             a.rows = L.rows;
+            a.rows_total = (int)rows;
+            a.mchunks = (int)div_up(rows, L.rows);
             a.x_kind = x_kind;
             a.x = x;
             if ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) {
@@ -518,7 +522,7 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
     const kh_weight &w = *weight;
     int unit = gemv_unit(w.format, w.group);
-    if (unit && rows <= (uint64_t)gemv_max_rows(1) && (uintptr_t)q % 4 == 0 && w.bytes < (1ull << 31)) {
+    if (unit && rows <= GEMV_ROWS && (uintptr_t)q % 4 == 0 && w.bytes < (1ull << 31)) {
         // The bytes go through the small-M product's own preparation.
         GemvArgs g{};
         g.count = 1;
@@ -528,14 +532,17 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
         uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
         g.row_bytes = k / len * size;
         g.k = (int)k;
-        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), (int)rows, 1);
+        const int chunk_rows = (int)std::min<uint64_t>(rows, gemv_max_rows(1));
+        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), chunk_rows, 1, (int)div_up(rows, chunk_rows));
         g.units = sp.units;
         g.chunk = sp.chunk;
         g.total_tiles = (int)div_up(w.n, 16);
         g.tiles = sp.tiles;
         g.tiles_log2 = g.tiles == 4 ? 2 : g.tiles == 2 ? 1 : 0;
         g.kw = sp.kw;
-        g.rows = (int)rows;
+        g.rows = chunk_rows;
+        g.rows_total = (int)rows;
+        g.mchunks = (int)div_up(rows, chunk_rows);
         g.x_kind = KH_I8_INTERNAL;
         g.x = q;
         g.dots = dots;

@@ -41,6 +41,8 @@ namespace {
 
 using lanes::v4i;
 
+constexpr int XCDS = 8;
+
 
 // How the kernel reads the activations: f32 (16-byte aligned), bf16 or f16
 // (8-byte aligned; which of the two is a runtime flag with no branch), or
@@ -93,6 +95,13 @@ __device__ __forceinline__ uint32_t pack_bytes(int a, int b, int c, int d) {
 // * the integer sum of the block's (or half's) values.
 constexpr int PASSES = 4;
 
+// The activations a workgroup prepares: rows [rows, k] at x, of kind x_kind.
+struct XIn {
+    const void *x;
+    int rows, k;
+    uint32_t kind;
+};
+
 // Cross-lane steps inside a block of 32 activations (8 lanes): DPP quad
 // permutations for lanes ^ 1 and ^ 2, ds_swizzle for lanes ^ 4.
 __device__ __forceinline__ int lane_xor1(int v) { return __builtin_amdgcn_mov_dpp(v, 0xb1, 0xf, 0xf, true); }
@@ -110,31 +119,31 @@ __device__ __forceinline__ void quad_at(int q, int qpr, int &m, int &eq) {
 }
 
 template <int XK>
-__device__ __forceinline__ void x_load(const GemvArgs &a, int e0, int span, int tid, int nthreads,
+__device__ __forceinline__ void x_load(const XIn &a, int e0, int span, int q0, int tid, int nthreads,
                                        float (&v)[PASSES][4]) {
     const int qpr = span / 4, quads = a.rows * qpr;
 #pragma unroll
     for (int i = 0; i < PASSES; i++) {
         // Every thread loads (from the last quad when it has none), so that
         // the loads issued after these can be counted on.
-        int q = tid + nthreads * i, m, eq;
+        int q = q0 + tid + nthreads * i, m, eq;
         quad_at(q, qpr, m, eq);
         int e = e0 + 4 * eq;
         bool in = q < quads && e < a.k;
-        x4<XK>(a.x, in ? (uint64_t)m * a.k + e : (uint64_t)a.rows * a.k - 4, a.x_kind == KH_BF16, v[i]);
+        x4<XK>(a.x, in ? (uint64_t)m * a.k + e : (uint64_t)a.rows * a.k - 4, a.kind == KH_BF16, v[i]);
         for (int j = 0; j < 4; j++) v[i][j] = in ? v[i][j] : 0.0f;
     }
 }
 
 template <int P, int XK>
-__device__ void x_prepare(const GemvArgs &a, int span, int tid, int nthreads, const float (&v)[PASSES][4],
-                          int8_t *planes, float4 *info) {
+__device__ void x_prepare(const XIn &a, int span, int q0, int tid, int nthreads,
+                          const float (&v)[PASSES][4], int8_t *planes, float4 *info) {
     const int qpr = span / 4, quads = a.rows * qpr;
     const int wave0 = tid & ~63;
 #pragma unroll
     for (int i = 0; i < PASSES; i++) {
-        if (nthreads * i + wave0 >= quads) break;  // nothing for this wave
-        int q = tid + nthreads * i, m, eq;
+        if (q0 + nthreads * i + wave0 >= quads) break;  // nothing for this wave
+        int q = q0 + tid + nthreads * i, m, eq;
         quad_at(q, qpr, m, eq);
         // The block's largest magnitude as an integer maximum of the bit
         // patterns (their order for non-negative floats); NaN and infinity
@@ -215,11 +224,24 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     constexpr int NG = F::GS == 16 ? F::STEPS : F::STEPS / 2;  // groups per unit and lane
     extern __shared__ __align__(16) uint8_t lds[];
 
+    // Workgroup -> (group of tiles, chunk of activation rows): the row chunks
+    // of a group of tiles are dispatched together and on one XCD, so that the
+    // weights the first reads are still in that XCD's L2 for the others.
+    const int b = blockIdx.x, local = b / XCDS;
+    const int mc = local % a.mchunks;
+    const int group = (local / a.mchunks) * XCDS + b % XCDS;
+    if (group * a.tiles >= a.total_tiles) return;
+    const int m0 = mc * a.rows;
+    const int rows = min(a.rows, a.rows_total - m0);
+    const XIn xin{static_cast<const uint8_t *>(a.x) + (size_t)m0 * a.k * (XK == X_F32 ? 4 : XK == X_H16 ? 2 : 1),
+                  rows, a.k, a.x_kind};
+    void *const out = static_cast<uint8_t *>(a.out) + (size_t)m0 * a.out_stride * (a.out_kind == KH_F32 ? 4 : 2);
+    int32_t *const dots = a.dots ? a.dots + (size_t)m0 * a.width * (a.k / 16) : nullptr;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, n16 = lane & 15;
     const int tl = wave & (a.tiles - 1), kw = wave >> a.tiles_log2;
-    const int tile = blockIdx.x * a.tiles + tl;
+    const int tile = group * a.tiles + tl;
     // Waves past the last tile load nothing (their offsets are NONE) and
     // write nothing.
     const bool any = tile < a.total_tiles;
@@ -246,9 +268,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     // LDS: planes [rows][P][span], zeros [span] (the A operand of lanes
     // outside their slice), info [rows][span / 32], sums [waves][16][rows].
     int8_t *planes = reinterpret_cast<int8_t *>(lds + 16);
-    int8_t *zeros = planes + (size_t)a.rows * P * span;
+    int8_t *zeros = planes + (size_t)rows * P * span;
     float4 *info = reinterpret_cast<float4 *>(zeros + span);
-    float *sums = reinterpret_cast<float *>(info + (size_t)a.rows * (span / 32));
+    float *sums = reinterpret_cast<float *>(info + (size_t)rows * (span / 32));
     for (int i = threadIdx.x; i < span / 16; i += blockDim.x)
         reinterpret_cast<v4i *>(zeros)[i] = v4i{0, 0, 0, 0};
 
@@ -265,7 +287,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
 #pragma unroll
     for (int mi = 0; mi < MT; mi++) {
         int m = P == 3 ? mi : 4 * mi + aj, p = P == 3 ? aj : 0;
-        bool on = a_lane && p < P && m < a.rows;
+        bool on = a_lane && p < P && m < rows;
         a_off[mi] = (on ? (m * P + p) * span : (int)(zeros - planes)) + F::xpos(g, 0);
     }
     const float4 *my_info = info + F::xpos(g, 0) / 32;
@@ -282,7 +304,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
             if (U == 128 && !ok) bw = v4i{0, 0, 0, 0};
             // Block dots in the codes of kapel-cpu/src/bytes.rs:282-353, where
             // Q6_K's are signed: stored - 32 in each byte.
-            if (F::BYTES == 210 && a.dots)
+            if (F::BYTES == 210 && dots)
                 for (int i = 0; i < 4; i++)
                     bw[i] = (int)((((uint32_t)bw[i] | 0x80808080u) - 0x20202020u) ^ 0x80808080u);
             if (F::GS == 16 || (s & 1) == 0)
@@ -305,10 +327,10 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
 #pragma unroll
                 for (int j = 0; j < (P == 3 ? 1 : 4); j++) {
                     int m = P == 3 ? mi : 4 * mi + j;
-                    if (m >= a.rows) continue;
-                    if (a.dots) {
+                    if (m >= rows) continue;
+                    if (dots) {
                         if (live)
-                            a.dots[((uint64_t)m * a.width + col) * (a.k / 16) + (u * U + F::xpos(g, s0)) / 16] =
+                            dots[((uint64_t)m * a.width + col) * (a.k / 16) + (u * U + F::xpos(g, s0)) / 16] =
                                 c[mi][j];
                         continue;
                     }
@@ -339,7 +361,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     // the activations before their first multiplication.  A barrier behind
     // weight loads would hold every wave back: once the weights stream, a
     // wave's loads wait to issue.
-    const int qpc = a.rows * span / 4;  // quads of a chunk
+    const int qpc = rows * span / 4;  // quads of a chunk
     const int npw = min((int)(blockDim.x >> 6), (qpc + 64 * PASSES - 1) / (64 * PASSES));
     const bool prep = wave < npw;
     int *ready = reinterpret_cast<int *>(lds);
@@ -350,9 +372,11 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         const int step = a.kw;
         if (c0) __syncthreads();  // the previous chunk's planes are consumed
         if (prep) {
-            float xv[PASSES][4];
-            x_load<XK>(a, c0 * U, span, threadIdx.x, 64 * npw, xv);
-            x_prepare<P, XK>(a, span, threadIdx.x, 64 * npw, xv, planes, info);
+            for (int q0 = 0; q0 < qpc; q0 += 64 * npw * PASSES) {
+                float xv[PASSES][4];
+                x_load<XK>(xin, c0 * U, span, q0, threadIdx.x, 64 * npw, xv);
+                x_prepare<P, XK>(xin, span, q0, threadIdx.x, 64 * npw, xv, planes, info);
+            }
             __builtin_amdgcn_wave_barrier();  // every lane's writes before the release
             if (lane == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -373,7 +397,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
             }
         }
     }
-    if (a.dots) return;
+    if (dots) return;
 
     // The four lane groups of each row, in a fixed tree; then the waves of a
     // tile in order.
@@ -387,19 +411,19 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         if (live && g == 0)
 #pragma unroll
             for (int i = 0; i < ACC; i++)
-                if (i < a.rows) store_out(a.out_kind, a.out, (uint64_t)i * a.out_stride + col, acc[i]);
+                if (i < rows) store_out(a.out_kind, out, (uint64_t)i * a.out_stride + col, acc[i]);
         return;
     }
     if (g == 0)
 #pragma unroll
         for (int i = 0; i < ACC; i++)
-            if (i < a.rows) sums[((kw * a.tiles + tl) * 16 + n16) * a.rows + i] = acc[i];
+            if (i < rows) sums[((kw * a.tiles + tl) * 16 + n16) * rows + i] = acc[i];
     __syncthreads();
     if (kw == 0 && live && g == 0) {
-        for (int i = 0; i < a.rows; i++) {
-            float v = sums[(tl * 16 + n16) * a.rows + i];
-            for (int w = 1; w < a.kw; w++) v = v + sums[((w * a.tiles + tl) * 16 + n16) * a.rows + i];
-            store_out(a.out_kind, a.out, (uint64_t)i * a.out_stride + col, v);
+        for (int i = 0; i < rows; i++) {
+            float v = sums[(tl * 16 + n16) * rows + i];
+            for (int w = 1; w < a.kw; w++) v = v + sums[((w * a.tiles + tl) * 16 + n16) * rows + i];
+            store_out(a.out_kind, out, (uint64_t)i * a.out_stride + col, v);
         }
     }
 }
@@ -411,7 +435,8 @@ hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
     int mt = P == 3 ? a.rows : (a.rows + 3) / 4;
     int waves = a.tiles * a.kw;
     size_t lds = gemv_lds(a.rows, P, a.chunk, F::U, waves);
-    dim3 grid((unsigned)((a.total_tiles + a.tiles - 1) / a.tiles)), block(64 * waves);
+    const int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
+    dim3 grid((unsigned)((groups + XCDS - 1) / XCDS * XCDS * a.mchunks)), block(64 * waves);
     if (waves < 1 || waves > gemv_max_waves(P, a.rows) || lds > 65536) return hipErrorInvalidValue;
     if (mt <= 1) hipLaunchKernelGGL((gemv_kernel<F, P, 1, P == 3 ? 16 : 8, XK>), grid, block, lds, s, a);
     else if (mt <= 2) hipLaunchKernelGGL((gemv_kernel<F, P, 2, 8, XK>), grid, block, lds, s, a);

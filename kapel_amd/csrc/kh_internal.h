@@ -87,9 +87,10 @@ struct GemvArgs {
     uint64_t row_bytes;
     int k, units, chunk;
     int total_tiles, tiles, tiles_log2, kw;  // tiles: 1, 2 or 4
-    int rows;                     // activation rows
+    int rows;                     // activation rows of a workgroup (of a row chunk)
+    int rows_total, mchunks;      // all activation rows, in mchunks chunks of `rows`
     uint32_t x_kind;
-    const void *x;                // [rows, k], aligned to 4 elements
+    const void *x;                // [rows_total, k], aligned to 4 elements
     uint32_t out_kind;
     void *out;                    // [rows, out_stride]
     uint64_t out_stride;

@@ -219,6 +219,8 @@ def main(which):
     for fmt, group in BYTE_FORMATS:
         case_bytes(fmt, group, 13, 1024, 1 if which == "quick" else 6)
     case_bytes(Q6K, 0, 40, 4096, 16)        # byte activations, 16 rows, four chunks
+    case_bytes(Q4K, 0, 20, 512, 40)         # byte activations, 40 rows: three row chunks
+    case_product(Q4_0, 0, 24, 256, 19)      # f32 activations, 19 rows: three row chunks
     if which == "all":
         for fmt, group in FORMATS:
             for rows in (3, 17):
