@@ -1,21 +1,22 @@
 #!/usr/bin/env python3
-"""Weight-read bandwidth of Kapel's product by quantized weights on one MI355X.
+"""Throughput of Kapel's product by quantized weights on one MI355X.
 
 A step is one decode layer of Llama-3.2-3B in Q4_K_M at M = 1 (BASELINE.json
-config 2): the four stacked products [q; k; v], o, [gate; up] and down, with
-f32 activations resident in HBM.  28 distinct copies of the layer's weights
-(1.77 GB, one per layer of the model) are walked in turn, so more than 512 MB
-is read between two reuses of any weight and the 256 MB Infinity Cache cannot
-serve them.  The 28 layers are one HIP graph; a run replays it.
+config 2): the four stacked products [q; k; v], o, [gate; up] and down, with f32
+activations resident in HBM.  28 distinct copies of the layer's weights (1.77
+GB, one per layer of the model) are walked in turn, so more than 512 MB is read
+between two reuses of any weight and the 256 MB Infinity Cache cannot serve
+them.  The 28 layers are one HIP graph; a run replays it.
 
     python bench.py [--gpus 1] [--steps 280] [--warmup 56]
 
-One JSON line: `value` is the whole job's weight bytes / time (GB/s);
-`roofline` is the [gate; up] product kernel's own duration from HIP events
-around each launch on its stream (activations prepared beforehand); `m64_bytes`
-is config 3 (the same layer, M = 64, byte activations: int8 MFMA TOPS);
-`cpu_baseline` is the oracle's f32 product (the restated kapel-cpu algorithm)
-on this host's cores.
+One JSON line.  `value` is the whole job's weight bytes / time (GB/s).
+`roofline` is the dominant kernel, the Q4_K M = 1 product on the [gate; up]
+call (28,311,552 weight bytes a launch), timed with HIP events around graph
+replays of that call alone on its stream; `traffic` comes from rocprofv3
+FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json.  `configs`
+holds the other BASELINE.json configurations (1, 3, 4, 5).  `cpu_baseline` is
+the oracle's f32 product (the restated kapel-cpu algorithm) on this host.
 """
 import argparse
 import json
@@ -35,6 +36,10 @@ LAYER = [("q", 3072, 3072, "q4k"), ("k", 1024, 3072, "q4k"), ("v", 1024, 3072, "
          ("o", 3072, 3072, "q4k"), ("gate", 8192, 3072, "q4k"), ("up", 8192, 3072, "q4k"),
          ("down", 3072, 8192, "q6k")]
 CALLS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
+# Config 4: Qwen3-8B layer in Q8_0.
+QWEN_LAYER = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+              ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+QWEN_CALLS = [("q", "k", "v"), ("o",), ("gate", "up"), ("down",)]
 
 
 def physical_cores():
@@ -57,18 +62,6 @@ def physical_cores():
     return max(1, min(n, allowed, 16))
 
 
-def build_layer(ka, synth, torch):
-    """One layer's weights: f32 ~ N(0, 0.02), seeded per matrix, quantized."""
-    fmts = {"q4k": ka.Q4K, "q6k": ka.Q6K}
-    host, nbytes = {}, 0
-    for i, (name, n, k, fmt) in enumerate(LAYER):
-        values = synth.normal(100 + i, n * k, 0.02)
-        data = ka.quantize(fmts[fmt], 0, values)
-        host[name] = (fmts[fmt], data, n, k)
-        nbytes += data.size
-    return host, nbytes
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,7 +70,10 @@ def main():
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-m64", action="store_true")
+    ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--profile", choices=["gateup", "copy"],
+                    help="only launch the [gate; up] call (or a 256 MiB device copy) "
+                         "20 times, for rocprofv3 counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -94,127 +90,210 @@ def main():
 
     hip = ka.Hip(0)
     dev = hip.device
-    host, layer_bytes = build_layer(ka, synth, torch)
+    op = ka.QuantizedMatmul()
+    fmts = {"q4k": ka.Q4K, "q6k": ka.Q6K}
+
+    if args.profile == "copy":
+        # A plain copy of known size: the reference point of FETCH_SIZE and
+        # WRITE_SIZE (268,435,456 bytes read and written per launch).
+        src = torch.empty(1 << 28, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        return
+
+    def values(seed, count):
+        """count weights ~ N(0, 0.02): 4 Mi seeded values, repeated (the
+        timing does not depend on the values; the parity tests use full
+        seeded matrices)."""
+        base = synth.normal(seed, min(count, 1 << 22), 0.02)
+        return np.resize(base, count) if count > base.size else base
+
+    def quantized_layer(spec, seed0, fmt_of):
+        host, nbytes = {}, 0
+        for i, (name, n, k, *rest) in enumerate(spec):
+            fmt = fmt_of(rest)
+            data = ka.quantize(fmt, 0, values(seed0 + i, n * k))
+            host[name] = (fmt, data, n, k)
+            nbytes += data.size
+        return host, nbytes
+
+    host, layer_bytes = quantized_layer(LAYER, 100, lambda r: fmts[r[0]])
     L = args.layers
-    # 28 distinct copies of the layer on the device.
-    layers = []
-    for l in range(L):
-        layers.append({name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
-                       for name, (fmt, data, n, k) in host.items()})
+    if args.profile == "gateup":
+        ws = [[ka.QuantizedTensor(torch.from_numpy(host[c][1]).to(dev), host[c][0], 0, host[c][2], host[c][3])
+               for c in ("gate", "up")] for _ in range(L)]
+        x = torch.from_numpy(synth.normal(9, 3072, 1.0).reshape(1, 3072)).to(dev)
+        o = torch.empty((1, 16384), device=dev)
+        for i in range(20):
+            hip.forward(op, [x] + ws[i % L], out=o)
+        torch.cuda.synchronize()
+        return
+    layers = [{name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
+               for name, (fmt, data, n, k) in host.items()} for _ in range(L)]
     torch.cuda.synchronize()
 
-    def make_inputs(rows):
+    def inputs_for(calls, host_w, rows, dtype=torch.float32, seed=7):
         xs, outs = [], []
-        for ci, call in enumerate(CALLS):
-            k = host[call[0]][3]
-            width = sum(host[c][2] for c in call)
-            x = torch.from_numpy(synth.normal(7 + ci, rows * k, 1.0).reshape(rows, k)).to(dev)
+        for ci, call in enumerate(calls):
+            k = host_w[call[0]][3]
+            width = sum(host_w[c][2] for c in call)
+            x = torch.from_numpy(synth.normal(seed + ci, rows * k, 1.0).reshape(rows, k)).to(dev, dtype)
             xs.append(x)
-            outs.append(torch.empty((rows, width), dtype=torch.float32, device=dev))
+            outs.append(torch.empty((rows, width), dtype=dtype, device=dev))
         return xs, outs
 
-    op = ka.QuantizedMatmul()
-
-    def step(layer, xs, outs):
-        for ci, call in enumerate(CALLS):
-            hip.forward(op, [xs[ci]] + [layer[c] for c in call], out=outs[ci])
-
-    def reserve_workspace(rows, byte):
+    def reserve(calls, layer, rows, byte):
         size = 0
-        for call in CALLS:
-            ws = [layers[0][c] for c in call]
+        for call in calls:
+            ws = [layer[c] for c in call]
             arr = (ka._Weight * len(ws))(*[w.weight() for w in ws])
             size = max(size, ka.lib().kh_qmatmul_workspace(
                 arr, len(ws), ws[0].k, rows, ka.BYTE_ACTIVATIONS if byte else 0))
         hip.workspace(size)
 
-    def capture(count, xs, outs):
+    def timed(step_fns, steps, warmup):
+        """Graph of len(step_fns) steps, checked against an eager run, then
+        `steps` steps timed with events; seconds per step."""
+        n = len(step_fns)
+        step_fns[-1]()
+        torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for l in range(count):
-                step(layers[l % L], xs, outs)
-        return g
-
-    def run_mode(rows, byte, steps, warmup):
-        hip.with_byte_activations(byte)
-        reserve_workspace(rows, byte)
-        xs, outs = make_inputs(rows)
-        # Eager reference of the last layer's outputs.
-        step(layers[(steps - 1) % L], xs, outs)
+            for fn in step_fns:
+                fn()
+        for _ in range(max(1, warmup // n)):
+            g.replay()
         torch.cuda.synchronize()
-        eager = [o.clone() for o in outs]
-        full = capture(L, xs, outs)
-        rest = steps % L
-        part = capture(rest, xs, outs) if rest else None
-
-        def replay(nsteps):
-            for _ in range(nsteps // L):
-                full.replay()
-            if nsteps % L:
-                assert part is not None and nsteps % L == rest
-                part.replay()
-
-        # Graph replays agree with the eager run, bit for bit, replay after replay.
-        for _ in range(2):
-            replay(steps)
-            torch.cuda.synchronize()
-            for a, b in zip(outs, eager):
-                assert torch.equal(a, b), "graph replay differs from the eager product"
-        for _ in range(max(1, warmup // L)):
-            full.replay()
+        reps = max(1, steps // n)
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(reps):
+            g.replay()
+        b.record()
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        replay(steps)
-        torch.cuda.synchronize()
-        seconds = time.perf_counter() - t0
-        hip.with_byte_activations(False)
-        return seconds, xs, outs
+        return a.elapsed_time(b) * 1e-3 / (reps * n), reps * n
 
-    steps = args.steps
-    seconds, xs, outs = run_mode(1, False, steps, args.warmup)
-    ms_per_step = seconds * 1e3 / steps
-    value = layer_bytes * steps / seconds / 1e9
-
-    # The dominant kernel: the [gate; up] product (28.3 MB of Q4_K), timed
-    # with events around each launch; its activations prepared by a first call.
-    gate_bytes = host["gate"][1].size + host["up"][1].size
+    # ---- config 2: the layer at M = 1 (value) ----------------------------------
     hip.with_byte_activations(False)
-    reserve_workspace(1, False)
-    x3, o3 = xs[2], outs[2]
-    hip.forward(op, [x3, layers[0]["gate"], layers[0]["up"]], out=o3)
-    torch.cuda.synchronize()
-    durations = []
-    for rep in range(4):
-        pairs = []
-        torch.cuda._sleep(int(2.0e7))  # keeps the GPU behind the host's launches
-        for l in range(L):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            hip.forward(op, [x3, layers[l]["gate"], layers[l]["up"]], out=o3,
-                        reuse_activations=True)
-            b.record()
-            pairs.append((a, b))
-        torch.cuda.synchronize()
-        if rep:
-            durations += [a.elapsed_time(b) for a, b in pairs]
-    kernel_ms = float(np.mean(durations))
-    achieved = gate_bytes / (kernel_ms * 1e-3) / 1e9
-    roofline = {"kernel": "qmv_kernel<Q4K, 3, 1> ([gate; up], 16384 x 3072 Q4_K, M = 1)",
-                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4),
-                "traffic": None, "algorithmic_bytes": gate_bytes,
-                "avg_launch_us": round(kernel_ms * 1e3, 2), "launches": len(durations)}
+    reserve(CALLS, layers[0], 1, False)
+    xs, outs = inputs_for(CALLS, host, 1)
 
-    m64 = None
-    if not args.no_m64:
-        s64, _, _ = run_mode(64, True, L * 2, L)
-        ops = 2 * 64 * sum(n * k for _, n, k, _ in LAYER)
-        t = s64 / (L * 2)
-        m64 = {"workload": "config 3: the same layer, M = 64, byte activations",
-               "ms_per_step": round(t * 1e3, 4),
-               "tops": round(ops / t / 1e12, 2),
-               "mfma_frac": round(ops / t / 1e12 / INT8_PEAK_TOPS, 4),
-               "weight_gbps": round(layer_bytes / t / 1e9, 1)}
+    def layer_step(l):
+        def run():
+            for ci, call in enumerate(CALLS):
+                hip.forward(op, [xs[ci]] + [layers[l][c] for c in call], out=outs[ci])
+        return run
+
+    # Graph replays agree with the eager product, bit for bit.
+    layer_step(L - 1)()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    sec, steps_done = timed([layer_step(l) for l in range(L)], args.steps, args.warmup)
+    for a_, b_ in zip(outs, eager):
+        assert torch.equal(a_, b_), "graph replay differs from the eager product"
+    value = layer_bytes / sec / 1e9
+
+    # ---- roofline: the [gate; up] call alone ------------------------------------
+    gate_bytes = host["gate"][1].size + host["up"][1].size
+    x3, o3 = xs[2], outs[2]
+
+    def gate_step(l):
+        return lambda: hip.forward(op, [x3, layers[l]["gate"], layers[l]["up"]], out=o3)
+
+    gsec, _ = timed([gate_step(l) for l in range(L)], 10 * L, L)
+    achieved = gate_bytes / gsec / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        traffic = json.load(open(tpath)).get("gemv_q4k_gateup_m1_bytes_per_launch")
+    roofline = {"kernel": "gemv_kernel<Q4K, planes 3, 1 MFMA/step, 16 waves, f32 x> "
+                          "([gate; up], 16384 x 3072 Q4_K, M = 1)",
+                "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
+                "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
+                "algorithmic_bytes_per_launch": gate_bytes,
+                "avg_launch_us": round(gsec * 1e6, 2),
+                "timing": "HIP events around graph replays of 28 launches (rotated weights)"}
+
+    configs = {}
+    if not args.no_configs:
+        # ---- config 3: the same layer, M = 64, byte activations ---------------
+        hip.with_byte_activations(True)
+        reserve(CALLS, layers[0], 64, True)
+        xs, outs = inputs_for(CALLS, host, 64)
+        s3, _ = timed([layer_step(l) for l in range(L)], 2 * L, L)
+        ops3 = 2 * 64 * sum(n * k for _, n, k, _ in LAYER)
+        configs["3"] = {"workload": "Llama-3.2-3B layer (Q4_K + Q6_K down), M = 64, byte activations",
+                        "ms_per_step": round(s3 * 1e3, 4), "tops": round(ops3 / s3 / 1e12, 2),
+                        "mfma_frac": round(ops3 / s3 / 1e12 / INT8_PEAK_TOPS, 4),
+                        "weight_gbps": round(layer_bytes / s3 / 1e9, 1)}
+        hip.with_byte_activations(False)
+
+        # ---- config 1: Q4_0 8192 x 2048, M = 1 ---------------------------------
+        d1 = ka.quantize(ka.Q4_0, 0, synth.normal(0, 8192 * 2048, 0.02))  # seed 0, as config 1 says
+        copies = max(2, int(1.2e9 // d1.size))
+        w1 = [ka.QuantizedTensor(torch.from_numpy(d1).to(dev), ka.Q4_0, 0, 8192, 2048)
+              for _ in range(copies)]
+        x1 = torch.from_numpy(synth.normal(1, 2048, 1.0).reshape(1, 2048)).to(dev)
+        o1 = torch.empty((1, 8192), device=dev)
+        s1, _ = timed([(lambda w=w: hip.forward(op, [x1, w], out=o1)) for w in w1], 4 * copies, copies)
+        configs["1"] = {"workload": "Q4_0 8192 x 2048, M = 1, f32 activations",
+                        "us_per_call": round(s1 * 1e6, 2), "weight_gbps": round(d1.size / s1 / 1e9, 1)}
+        del w1
+
+        # ---- config 5: low-bit FFN, int4 attention, Q6_K output table, M in {1, 8}
+        c5 = {}
+        parts = [("up_q2k", ka.Q2K, 0, 12288, 4096), ("down_q2k", ka.Q2K, 0, 4096, 12288),
+                 ("up_q3k", ka.Q3K, 0, 12288, 4096), ("down_q3k", ka.Q3K, 0, 4096, 12288),
+                 ("up_q5k", ka.Q5K, 0, 12288, 4096), ("down_q5k", ka.Q5K, 0, 4096, 12288),
+                 ("q_int4", ka.INT4, 32, 4096, 4096)]
+        for name, fmt, group, n, k in parts:
+            d = ka.quantize(fmt, group, values(500 + len(c5), n * k))
+            copies = max(2, int(1.2e9 // d.size))
+            ws5 = [ka.QuantizedTensor(torch.from_numpy(d).to(dev), fmt, group, n, k) for _ in range(copies)]
+            for rows in (1, 8):
+                x5 = torch.from_numpy(synth.normal(5, rows * k, 1.0).reshape(rows, k)).to(dev)
+                o5 = torch.empty((rows, n), device=dev)
+                reserve([("w",)], {"w": ws5[0]}, rows, False)
+                s5, _ = timed([(lambda w=w: hip.forward(op, [x5, w], out=o5)) for w in ws5], 4 * copies, copies)
+                c5[f"{name}_m{rows}"] = {"us": round(s5 * 1e6, 2), "gbps": round(d.size / s5 / 1e9, 1)}
+            del ws5
+        table = ka.quantize(ka.Q6K, 0, values(77, 151936 * 4096))
+        wt = ka.QuantizedTensor(torch.from_numpy(table).to(dev), ka.Q6K, 0, 151936, 4096)
+        for rows in (1, 8):
+            xt = torch.from_numpy(synth.normal(6, rows * 4096, 1.0).reshape(rows, 4096)).to(dev)
+            ot = torch.empty((rows, 151936), device=dev)
+            reserve([("w",)], {"w": wt}, rows, False)
+            st, _ = timed([lambda: hip.forward(op, [xt, wt], out=ot)], 20, 4)
+            c5[f"table_q6k_m{rows}"] = {"us": round(st * 1e6, 2), "gbps": round(table.size / st / 1e9, 1)}
+        configs["5"] = {"workload": "Q2_K/Q3_K/Q5_K FFN (12288x4096, 4096x12288), int4/32 4096x4096, "
+                                    "Q6_K output table 151936x4096; f32 x; weights from 4 Mi N(0, 0.02) values repeated",
+                        "calls": c5}
+        del wt
+
+        # ---- config 4: Qwen3-8B layer, Q8_0, M = 512, bf16 activations in bytes
+        qhost, qbytes = quantized_layer(QWEN_LAYER, 300, lambda r: ka.Q8_0)
+        qlayers = [{name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
+                    for name, (fmt, data, n, k) in qhost.items()} for _ in range(2)]
+        hip.with_byte_activations(True)
+        reserve(QWEN_CALLS, qlayers[0], 512, True)
+        xq, oq = inputs_for(QWEN_CALLS, qhost, 512, dtype=torch.bfloat16)
+
+        def qwen_step(l):
+            def run():
+                for ci, call in enumerate(QWEN_CALLS):
+                    hip.forward(op, [xq[ci]] + [qlayers[l][c] for c in call], out=oq[ci])
+            return run
+
+        s4, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
+        hip.with_byte_activations(False)
+        ops4 = 2 * 512 * sum(n * k for _, n, k in QWEN_LAYER)
+        configs["4"] = {"workload": "Qwen3-8B layer in Q8_0, M = 512, bf16 activations quantized to bytes",
+                        "ms_per_step": round(s4 * 1e3, 3), "tops": round(ops4 / s4 / 1e12, 2),
+                        "mfma_frac": round(ops4 / s4 / 1e12 / INT8_PEAK_TOPS, 4),
+                        "weight_gbps": round(qbytes / s4 / 1e9, 1)}
+        del qlayers
 
     cpu = None
     if not args.no_cpu:
@@ -239,14 +318,14 @@ def main():
                          "kapel-cpu's portable quantized product"}
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-            "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+            "steps": steps_done, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "int8 (i8 x i8 -> i32 MFMA dots, f32 scales)", "data": "synthetic",
             "config": {"workload": "config 2: Llama-3.2-3B decode layer, Q4_K (q, k, v, o, "
                                    "gate, up) + Q6_K (down), M = 1, f32 activations",
                        "weight_bytes_per_step": layer_bytes, "layers_rotated": L,
                        "frac_of_hbm_peak": round(value / HBM_PEAK_GBPS, 4)},
-            "roofline": roofline, "m64_bytes": m64, "cpu_baseline": cpu}
+            "roofline": roofline, "configs": configs, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)
 
 

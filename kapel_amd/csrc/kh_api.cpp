@@ -106,7 +106,7 @@ struct GemvSplit {
     int units, chunk, tiles, kw;
 };
 
-GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int mchunks) {
+GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int mchunks, bool copied) {
     GemvSplit g{};
     g.units = (int)div_up(k, unit);
     g.tiles = 4;
@@ -114,7 +114,8 @@ GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int 
     g.kw = std::max(1, std::min(gemv_max_waves(planes, rows) / g.tiles, g.units));
     if (getenv("KH_TUNE_KW")) g.kw = std::max(1, std::min(atoi(getenv("KH_TUNE_KW")), gemv_max_waves(planes, rows) / g.tiles));
     int threads = 64 * g.tiles * g.kw;
-    int by_threads = 16 * threads / (rows * unit);
+    // Activations copied (prepared beforehand) are not limited by the threads.
+    int by_threads = copied ? 1 << 30 : 16 * threads / (rows * unit);
     // LDS: 16 + span (rows planes + 1 + rows / 2) + waves 64 rows <= 64 KiB.
     long room = 65536 - 16 - 64L * g.tiles * g.kw * rows;
     int by_lds = (int)(room / ((long)unit * rows * planes + unit + (long)unit * rows / 2));
@@ -161,6 +162,7 @@ struct Checked {
     uint64_t width = 0, max_wgs = 0, partial_floats = 0;
     bool bytes = false;
     bool any_qmv = false;  // a launch of the many-row product (prepared activations)
+    bool gemv_prep = false;  // a small-M launch in row chunks (prepared activations)
 };
 
 // One launch of the MFMA product: weights `members` (one format), rows
@@ -206,7 +208,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
             L.gemv = true;
             L.r0 = 0;
             L.rows = (int)std::min<uint64_t>(rows, gemv_max_rows(planes));
-            L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes, (int)div_up(rows, L.rows));
+            L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes, (int)div_up(rows, L.rows), L.rows < (int)rows);
             fn(L);
             continue;
         }
@@ -251,7 +253,10 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
     if (c.max_wgs > MAX_COUNTERS) return KH_ERR_OVERFLOW;
     if (k > 0 && rows > 0)
         each_launch(weights, count, k, rows, c.bytes ? 1 : 3, [&](const Launch &L) {
-            if (L.gemv) return;
+            if (L.gemv) {
+                c.gemv_prep = c.gemv_prep || L.rows < (int)rows;
+                return;
+            }
             c.any_qmv = true;
             if (L.split.segs > 1)
                 c.partial_floats = std::max<uint64_t>(
@@ -267,7 +272,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     int planes = c.bytes ? 1 : 3;
     hipError_t err;
     // The activations, once for all weights.
-    if (c.any_qmv && !reuse) {
+    if ((c.any_qmv || c.gemv_prep) && !reuse) {
         PrepArgs p{};
         p.x_kind = x_kind;
         p.x = x;
@@ -337,9 +342,20 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.rows = L.rows;
             a.rows_total = (int)rows;
             a.mchunks = (int)div_up(rows, L.rows);
+            a.hi = 65536.0f;
+            a.shift = 8;
+            if (a.mchunks > 1) {
+                a.pplanes = reinterpret_cast<const int8_t *>(ws + l.planes_off);
+                a.pkpad = l.kpad;
+                a.pxscale = reinterpret_cast<const float *>(ws + l.xscale_off);
+                a.pxsum32 = reinterpret_cast<const float *>(ws + l.xsum32_off);
+                a.pxsum16 = reinterpret_cast<const float *>(ws + l.xsum16_off);
+                a.hi = 16384.0f;
+                a.shift = 7;
+            }
             a.x_kind = x_kind;
             a.x = x;
-            if ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) {
+            if (a.mchunks == 1 && (uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) {
                 void *copy = ws + l.xcopy_off;
                 hipError_t e = hipMemcpyAsync(copy, x, rows * k * kind_bytes(x_kind),
                                               hipMemcpyDeviceToDevice, s);
@@ -533,7 +549,7 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
         g.row_bytes = k / len * size;
         g.k = (int)k;
         const int chunk_rows = (int)std::min<uint64_t>(rows, gemv_max_rows(1));
-        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), chunk_rows, 1, (int)div_up(rows, chunk_rows));
+        GemvSplit sp = gemv_split(k, unit, (int)div_up(w.n, 16), chunk_rows, 1, (int)div_up(rows, chunk_rows), false);
         g.units = sp.units;
         g.chunk = sp.chunk;
         g.total_tiles = (int)div_up(w.n, 16);

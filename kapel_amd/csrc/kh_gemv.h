@@ -336,7 +336,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
                     }
                     float4 in = my_info[(size_t)m * (span / 32) + blk];
                     float dot;
-                    if (P == 3) dot = fmaf((float)c[mi].x, 65536.0f, (float)(c[mi].y * 256 + c[mi].z));
+                    if (P == 3) dot = fmaf((float)c[mi].x, a.hi, (float)((c[mi].y << a.shift) + c[mi].z));
                     else dot = (float)c[mi][j];
                     float xsum = F::GS == 32 ? in.y : (second ? in.w : in.z);
                     float t = fmaf(dot, sc[gi] * in.x, acc[m]);
@@ -371,7 +371,32 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         const int c1 = min(a.units, c0 + a.chunk);
         const int step = a.kw;
         if (c0) __syncthreads();  // the previous chunk's planes are consumed
-        if (prep) {
+        if (prep && a.pplanes) {
+            // Copy this chunk of the prepared activations, row by row.
+            const int nt = 64 * npw, kb = a.k / 32;
+            for (int m = 0; m < rows; m++)
+                for (int p = 0; p < P; p++) {
+                    const int8_t *src = a.pplanes + ((size_t)(m0 + m) * P + p) * a.pkpad;
+                    int8_t *dst = planes + (size_t)(m * P + p) * span;
+                    for (int w = threadIdx.x; w < span / 4; w += nt) {
+                        const int e = c0 * U + 4 * w;
+                        *reinterpret_cast<uint32_t *>(dst + 4 * w) =
+                            e < a.k ? *reinterpret_cast<const uint32_t *>(src + e) : 0u;
+                    }
+                }
+            for (int m = 0; m < rows; m++) {
+                const size_t r = (size_t)(m0 + m);
+                for (int blk = threadIdx.x; blk < span / 32; blk += nt) {
+                    const int bk = c0 * U / 32 + blk;
+                    info[(size_t)m * (span / 32) + blk] =
+                        bk < kb ? float4{a.pxscale[r * kb + bk], a.pxsum32[r * kb + bk],
+                                         a.pxsum16[r * 2 * kb + 2 * bk], a.pxsum16[r * 2 * kb + 2 * bk + 1]}
+                                : float4{0.0f, 0.0f, 0.0f, 0.0f};
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            if (lane == 0) __hip_atomic_fetch_add(ready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else if (prep) {
             for (int q0 = 0; q0 < qpc; q0 += 64 * npw * PASSES) {
                 float xv[PASSES][4];
                 x_load<XK>(xin, c0 * U, span, q0, threadIdx.x, 64 * npw, xv);

@@ -96,6 +96,15 @@ struct GemvArgs {
     uint64_t out_stride;
     int32_t *dots;                // block dots [rows, width, k / 16] instead of out
     uint64_t width;
+    // Activations prepared beforehand (prep_x_kernel) for all rows, copied
+    // instead of prepared by each workgroup; NULL: prepared in the kernel.
+    const int8_t *pplanes;        // [rows_total][P][pkpad]
+    uint64_t pkpad;
+    const float *pxscale, *pxsum32, *pxsum16;  // [rows_total][k / 32, k / 32, k / 16]
+    // The planes' digits: v = a hi + (b << shift) + c (prep_x_kernel: 2^14,
+    // 7; the kernel's own preparation: 2^16, 8).
+    float hi;
+    int shift;
 };
 
 struct GenericArgs {
