@@ -112,7 +112,6 @@ GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int 
     g.tiles = 4;
     while (g.tiles > 1 && div_up(tiles, g.tiles) * mchunks < 256) g.tiles /= 2;
     g.kw = std::max(1, std::min(gemv_max_waves(planes, rows) / g.tiles, g.units));
-    if (getenv("KH_TUNE_KW")) g.kw = std::max(1, std::min(atoi(getenv("KH_TUNE_KW")), gemv_max_waves(planes, rows) / g.tiles));
     int threads = 64 * g.tiles * g.kw;
     // Activations copied (prepared beforehand) are not limited by the threads.
     int by_threads = copied ? 1 << 30 : 16 * threads / (rows * unit);
@@ -121,6 +120,31 @@ GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int 
     int by_lds = (int)(room / ((long)unit * rows * planes + unit + (long)unit * rows / 2));
     g.chunk = std::max(1, std::min({g.units, by_threads, by_lds}));
     return g;
+}
+
+// The many-row product's split, a function of the shapes only: 64 activation
+// rows a workgroup with bytes (32 with three planes), column groups of 256
+// weight rows, and K split into `ks` ranges of `ups` units when the row and
+// column tiles give fewer than 256 workgroups (one a CU: a workgroup fills its
+// CU's registers).  Each range keeps at least 512 elements of K.
+struct MmSplit {
+    int wm, mtiles, ngroups, units, ups, ks;
+};
+
+constexpr int MM_COLS = 256;
+
+MmSplit mm_split(uint64_t rows, uint64_t k, int unit, int planes, int ngroups) {
+    MmSplit m{};
+    m.wm = planes == 1 && rows > 32 ? 2 : 1;
+    m.mtiles = (int)div_up(rows, 32 * m.wm);
+    m.ngroups = ngroups;
+    m.units = (int)div_up(k, unit);
+    uint64_t base = (uint64_t)m.mtiles * ngroups;
+    int most = std::max(1, m.units / (int)div_up(512, unit));
+    int ks = (int)std::min<uint64_t>(most, std::max<uint64_t>(1, div_up(256, base)));
+    m.ups = (int)div_up(m.units, ks);
+    m.ks = (int)div_up(m.units, m.ups);
+    return m;
 }
 
 // The workspace: the counters of the segment split (fixed, first), the
@@ -173,8 +197,10 @@ struct Launch {
     uint64_t r0;
     int rows;
     bool gemv;        // the small-M product (all rows in one launch)
+    bool mm;          // the many-row product (rows r0 .. r0 + rows)
     GemvSplit gsplit;
     Split split;
+    MmSplit msplit;
 };
 
 // Every launch of a product, in order: the weights of a format and group,
@@ -204,7 +230,9 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         // The small-M product reads each matrix at 32-bit offsets.
         bool offsets32 = true;
         for (uint32_t m : L.members) offsets32 = offsets32 && weights[m].bytes < (1ull << 31);
-        if (unit && offsets32 && rows <= GEMV_ROWS) {
+        L.mm = false;
+        bool one_chunk = rows <= (uint64_t)gemv_max_rows(planes);
+        if (unit && offsets32 && (one_chunk || (rows <= GEMV_ROWS && !mm_group(w.format, w.group)))) {
             L.gemv = true;
             L.r0 = 0;
             L.rows = (int)std::min<uint64_t>(rows, gemv_max_rows(planes));
@@ -213,6 +241,22 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
             continue;
         }
         L.gemv = false;
+        if (unit && offsets32 && mm_group(w.format, w.group)) {
+            // Launches of at most 2 GiB of prepared activations each.
+            L.mm = true;
+            uint64_t kpad = align_up(std::max<uint64_t>(k, 64), 64);
+            uint64_t fit = ((1ull << 31) - 1) / ((uint64_t)planes * kpad) / 64 * 64;
+            int ngroups = 0;
+            for (uint32_t m : L.members) ngroups += (int)div_up(weights[m].n, MM_COLS);
+            for (uint64_t r0 = 0; r0 < rows; r0 += fit) {
+                L.r0 = r0;
+                L.rows = (int)std::min<uint64_t>(fit, rows - r0);
+                L.msplit = mm_split((uint64_t)L.rows, k, unit, planes, ngroups);
+                fn(L);
+            }
+            continue;
+        }
+        L.mm = false;
         int chunk = rows_per_launch(w.format, planes);
         for (uint64_t r0 = 0; r0 < rows; r0 += chunk) {
             L.r0 = r0;
@@ -258,6 +302,12 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
                 return;
             }
             c.any_qmv = true;
+            if (L.mm) {
+                if (L.msplit.ks > 1)
+                    c.partial_floats = std::max<uint64_t>(c.partial_floats,
+                                                          (uint64_t)L.msplit.ks * L.rows * c.width);
+                return;
+            }
             if (L.split.segs > 1)
                 c.partial_floats = std::max<uint64_t>(
                     c.partial_floats, (uint64_t)L.split.segs * L.rows * L.tiles * 16);
@@ -350,8 +400,6 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
                 a.pxscale = reinterpret_cast<const float *>(ws + l.xscale_off);
                 a.pxsum32 = reinterpret_cast<const float *>(ws + l.xsum32_off);
                 a.pxsum16 = reinterpret_cast<const float *>(ws + l.xsum16_off);
-                a.hi = 16384.0f;
-                a.shift = 7;
             }
             a.x_kind = x_kind;
             a.x = x;
@@ -370,6 +418,48 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.out_stride = c.width;
             a.width = c.width;
             err = launch_gemv(w.format, w.group, planes, a, s);
+            return;
+        }
+        if (L.mm) {
+            MmArgs a{};
+            a.count = (int)L.members.size();
+            int ng = 0;
+            for (int m = 0; m < a.count; m++) {
+                const kh_weight &wm = weights[L.members[m]];
+                a.w[m] = static_cast<const uint8_t *>(wm.data);
+                a.wbytes[m] = (uint32_t)wm.bytes;
+                a.n[m] = wm.n;
+                a.col0[m] = col0[L.members[m]];
+                a.ng0[m] = ng;
+                ng += (int)div_up(wm.n, MM_COLS);
+            }
+            uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
+            const int g = mm_group(w.format, w.group);
+            a.row_bytes = k / len * size;
+            a.k = (int)k;
+            a.units = L.msplit.units;
+            a.ups = L.msplit.ups;
+            a.ks = L.msplit.ks;
+            a.ngroups = L.msplit.ngroups;
+            a.mtiles = L.msplit.mtiles;
+            a.wm = L.msplit.wm;
+            a.rows = L.rows;
+            const uint64_t r0 = L.r0;
+            a.planes = reinterpret_cast<const int8_t *>(ws + l.planes_off) + r0 * planes * l.kpad;
+            a.planes_bytes = (uint32_t)((uint64_t)L.rows * planes * l.kpad);
+            a.kpad = l.kpad;
+            a.xscale = reinterpret_cast<const float *>(ws + l.xscale_off) + r0 * (k / 32);
+            a.xsum = g == 16 ? reinterpret_cast<const float *>(ws + l.xsum16_off) + r0 * (k / 16)
+                             : reinterpret_cast<const float *>(ws + l.xsum32_off) + r0 * (k / 32);
+            a.hi = 65536.0f;
+            a.shift = 8;
+            a.out_kind = out_kind;
+            a.out = static_cast<uint8_t *>(out) + r0 * c.width * kind_bytes(out_kind);
+            a.out_stride = c.width;
+            a.width = c.width;
+            a.partials = reinterpret_cast<float *>(ws + l.partials_off);
+            err = launch_mm(w.format, w.group, planes, a, s);
+            if (err == hipSuccess && a.ks > 1) err = launch_mm_reduce(a, s);
             return;
         }
         QmvArgs a{};

@@ -101,10 +101,36 @@ struct GemvArgs {
     const int8_t *pplanes;        // [rows_total][P][pkpad]
     uint64_t pkpad;
     const float *pxscale, *pxsum32, *pxsum16;  // [rows_total][k / 32, k / 32, k / 16]
-    // The planes' digits: v = a hi + (b << shift) + c (prep_x_kernel: 2^14,
-    // 7; the kernel's own preparation: 2^16, 8).
+    // The planes' digits: v = a hi + (b << shift) + c (2^16, 8).
     float hi;
     int shift;
+};
+
+// The many-row product (kh_mm.h): weights of one format in column groups of
+// 256 rows; a workgroup takes one group, 32 or 64 activation rows (`wm`
+// tiles of 32) and one of `ks` splits of K (`ups` units each).
+struct MmArgs {
+    int count;
+    const uint8_t *w[MAX_WEIGHTS];
+    uint32_t wbytes[MAX_WEIGHTS];  // bytes of each matrix (< 2 GiB)
+    uint64_t n[MAX_WEIGHTS];
+    uint64_t col0[MAX_WEIGHTS];
+    int ng0[MAX_WEIGHTS];          // first column group of each weight
+    uint64_t row_bytes;
+    int k, units, ups, ks, ngroups, mtiles, wm;
+    int rows;                      // activation rows of this launch
+    // Prepared activations of these rows (prep_x_kernel).
+    const int8_t *planes;          // [rows][P][kpad]
+    uint32_t planes_bytes;         // < 2 GiB
+    uint64_t kpad;
+    const float *xscale;           // [rows][k / 32]
+    const float *xsum;             // [rows][k / G]: the sums of the format's groups
+    float hi;                      // three planes: v = a hi + (b << shift) + c
+    int shift;
+    uint32_t out_kind;
+    void *out;                     // [rows, out_stride]
+    uint64_t out_stride, width;
+    float *partials;               // [ks][rows][width] when ks > 1
 };
 
 struct GenericArgs {
@@ -139,6 +165,11 @@ int gemv_max_waves(int planes, int rows);
 // Bytes of LDS of one of its workgroups.
 size_t gemv_lds(int rows, int planes, int chunk, int unit, int waves);
 hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s);
+// The many-row product: the size of a format's scale groups (32 or 16; 0:
+// not read by it).
+int mm_group(uint32_t fmt, uint32_t group);
+hipError_t launch_mm(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s);
+hipError_t launch_mm_reduce(const MmArgs &a, hipStream_t s);
 hipError_t launch_generic(const GenericArgs &a, hipStream_t s);
 hipError_t launch_dequantize(const DequantArgs &a, hipStream_t s);
 

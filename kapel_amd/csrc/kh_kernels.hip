@@ -5,11 +5,11 @@
 //  1. prep_x: the activations, by blocks of 32, become int8 "planes" in the
 //     workspace.  With byte activations (kapel-cpu/src/bytes.rs:144-158) the
 //     one plane is the CPU's q and the block scale its s.  With f32
-//     activations, each block is a 21-bit fixed-point number x * 2^sh
-//     (sh = 20 - exponent of the block's largest magnitude), split into three
-//     signed 7-bit digits (planes) a * 2^14 + b * 2^7 + c: the integer dots of
-//     the three planes recompose the dot exactly, and the representation
-//     error is below 2^-21 of the block's largest value.
+//     activations, each block is a 23-bit fixed-point number x * 2^sh
+//     (sh = 22 - exponent of the block's largest magnitude), split into three
+//     signed bytes (planes) a * 2^16 + b * 2^8 + c: the integer dots of the
+//     three planes recompose the dot, and the representation error is below
+//     2^-23 of the block's largest value.
 //
 //  2. qmv: each wave takes 16 weight rows and a segment of K.  Per step of 64
 //     elements it unpacks the weights' codes in registers into bytes (the B
@@ -85,18 +85,19 @@ __global__ __launch_bounds__(256) void prep_x_kernel(PrepArgs a) {
         r = r != r ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
         value = digit[0] = (int)r;
     } else {
-        // 21-bit fixed point against the block's largest magnitude, in three
-        // signed digits: value = d0 * 2^14 + d1 * 2^7 + d2, |d1|, |d2| <= 64.
+        // 23-bit fixed point against the block's largest magnitude, in three
+        // signed bytes: value = d0 * 2^16 + d1 * 2^8 + d2, |value| <= 2^22,
+        // |d0| <= 64.
         bool finite = isfinite(max);
         int exponent = 0;
         if (max > 0.0f && finite) frexpf(max, &exponent);  // max < 2^exponent
-        int sh = 20 - exponent;
+        int sh = 22 - exponent;
         float f = (max > 0.0f && finite) ? rintf(__builtin_ldexpf(v, sh)) : 0.0f;
         value = f != f ? 0 : (int)f;
-        int c = ((value + 64) & 127) - 64;
-        int r1 = (value - c) >> 7;
-        int b = ((r1 + 64) & 127) - 64;
-        digit[0] = (r1 - b) >> 7;
+        int c = ((value + 128) & 255) - 128;
+        int r1 = (value - c) >> 8;
+        int b = ((r1 + 128) & 255) - 128;
+        digit[0] = (r1 - b) >> 8;
         digit[1] = b;
         digit[2] = c;
         // A block holding a NaN or an infinity gives NaN, as the product does.
@@ -257,8 +258,8 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                     int osg = q * 4 + g;
                     if (osg < nsg) {
                         int m = osg / F::NGRP, grp = osg % F::NGRP;
-                        // d0 2^14 + d1 2^7 + d2, in wrapping unsigned arithmetic
-                        int dot = (int)(((uint32_t)c.x << 14) + ((uint32_t)c.y << 7) + (uint32_t)c.z);
+                        // d0 2^16 + d1 2^8 + d2 (the last two fit an int).
+                        float dot = fmaf((float)c.x, 65536.0f, (float)((c.y << 8) + c.z));
                         bool present = two || F::gelem(t, grp) < a.k;
                         if (present) {
                             float s, mn;
@@ -267,7 +268,7 @@ __global__ __launch_bounds__(256) void qmv_kernel(QmvArgs a) {
                             float xsc = xs[m * (span / 32) + ge / 32];
                             float xsum = F::GS == 32 ? xs32[m * (span / 32) + ge / 32]
                                                      : xs16[m * (span / 16) + ge / 16];
-                            acc[q][0] = fmaf((float)dot, s * xsc, acc[q][0]);
+                            acc[q][0] = fmaf(dot, s * xsc, acc[q][0]);
                             acc[q][0] = fmaf(-mn, xsum, acc[q][0]);
                         }
                     }

@@ -1,0 +1,17 @@
+// Instances of the many-row product (kh_mm.h): the 256-element super-blocks, Q2_K to Q6_K.
+#include "kh_mm.h"
+
+namespace kh {
+
+hipError_t mm_kquants(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s) {
+    switch (fmt) {
+    case KH_Q4K: return mm::launch_f<mm::Q4K>(a, planes, s);
+    case KH_Q5K: return mm::launch_f<mm::Q5K>(a, planes, s);
+    case KH_Q6K: return mm::launch_f<mm::Q6K>(a, planes, s);
+    case KH_Q2K: return mm::launch_f<mm::Q2K>(a, planes, s);
+    case KH_Q3K: return mm::launch_f<mm::Q3K>(a, planes, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace kh

@@ -111,6 +111,62 @@ inline v4i mfma_i8(v4i a, v4i b, v4i c, int, int, int) {
     return d;
 }
 
+typedef int v16i __attribute__((ext_vector_type(16)));
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+// The 32 x 32 MFMAs: lane l supplies row l % 32 of A and column l % 32 of B
+// for the k-slice l / 32 (B bytes, or one f32, per lane), and receives
+// D[8 (v / 4) + 4 (l / 32) + v % 4][l % 32], v = 0..15.
+inline int row32(int l, int v) { return 8 * (v / 4) + 4 * (l / 32) + v % 4; }
+
+template <int B>
+inline v16i mfma32_i8(const void *a, const void *b, v16i c) {
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], a, B);
+    std::memcpy(&block.slots[w][l][2], b, B);
+    wave_sync();
+    v16i d = c;
+    int j = l % 32;
+    for (int v = 0; v < 16; v++) {
+        int i = row32(l, v), sum = 0;
+        for (int half = 0; half < 2; half++) {
+            const int8_t *ai = reinterpret_cast<const int8_t *>(&block.slots[w][32 * half + i][0]);
+            const int8_t *bj = reinterpret_cast<const int8_t *>(&block.slots[w][32 * half + j][2]);
+            for (int k = 0; k < B; k++) sum += (int)ai[k] * (int)bj[k];
+        }
+        d[v] += sum;
+    }
+    wave_sync();
+    return d;
+}
+inline v16i mfma32_i8x32(v4i a, v4i b, v16i c, int, int, int) { return mfma32_i8<16>(&a, &b, c); }
+inline v16i mfma32_i8x16(long a, long b, v16i c, int, int, int) { return mfma32_i8<8>(&a, &b, c); }
+
+inline v16f mfma32_f32x2(float a, float b, v16f c, int, int, int) {
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &a, 4);
+    std::memcpy(&block.slots[w][l][2], &b, 4);
+    wave_sync();
+    v16f d = c;
+    int j = l % 32;
+    for (int v = 0; v < 16; v++) {
+        int i = row32(l, v);
+        // The hardware's sum of the two products: emulated as f64 products
+        // summed then rounded once, then added to C (both products here are
+        // exact in f32 whenever one k-slot is zero).
+        float sum = 0.0f;
+        for (int half = 0; half < 2; half++) {
+            float ai, bj;
+            std::memcpy(&ai, &block.slots[w][32 * half + i][0], 4);
+            std::memcpy(&bj, &block.slots[w][32 * half + j][2], 4);
+            sum += ai * bj;
+        }
+        d[v] += sum;
+    }
+    wave_sync();
+    return d;
+}
+
 // v_perm_b32: byte s of the result is byte sel[s] of {hi:lo} (0..3 of lo,
 // 4..7 of hi); selectors above 7 are not used by the kernels.
 inline uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
@@ -203,6 +259,9 @@ void launch(K kernel, dim3 grid, dim3 threads, size_t lds, A... args);
 
 namespace kh {
 alignas(16) inline uint8_t lds[emu::LDS_BYTES];
+namespace mm {
+alignas(16) inline uint8_t lds[emu::LDS_BYTES];
+}
 }
 
 #define threadIdx (emu::self.tid)
@@ -212,6 +271,11 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define __threadfence() __atomic_thread_fence(__ATOMIC_SEQ_CST)
 #define __shfl_xor(v, m, ...) emu::shfl_xor((v), (m) __VA_OPT__(, ) __VA_ARGS__)
 #define __builtin_amdgcn_mfma_i32_16x16x64_i8(...) emu::mfma_i8(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_i32_32x32x32_i8(...) emu::mfma32_i8x32(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_i32_32x32x16_i8(...) emu::mfma32_i8x16(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_f32_32x32x2f32(...) emu::mfma32_f32x2(__VA_ARGS__)
+#define __builtin_amdgcn_sched_barrier(m) ((void)0)
+#define KH_PIN(x) ((void)0)
 #define __builtin_amdgcn_perm(hi, lo, s) emu::perm((hi), (lo), (s))
 #define __builtin_amdgcn_alignbyte(hi, lo, s) emu::alignbyte((hi), (lo), (s))
 #define __builtin_amdgcn_mov_dpp(v, c, r, b, z) emu::mov_dpp((v), (c), (r), (b), (z))

@@ -116,7 +116,7 @@ def case_product(fmt, group, n, k, rows, seed=5):
               ko.product_f64([(fmt, group, d, n)], k, x))
 
 
-def case_bytes(fmt, group, n, k, rows):
+def case_bytes(fmt, group, n, k, rows, dots=True):
     d = blocks(fmt, group, n * k // ko.block_len(fmt, group), 3)
     i = np.arange(rows * k)
     x = ((((i * 7919) % 201).astype(np.float32) / np.float32(100.0) - np.float32(1.0))
@@ -126,10 +126,11 @@ def case_bytes(fmt, group, n, k, rows):
     w = W(fmt, group, d.ctypes.data, d.size, n)
     size = L.kh_qmatmul_workspace(ctypes.byref(w), 1, k, rows, 1)
     ws = workspace(size)
-    dots = np.zeros((rows, n, k // 16), np.int32)
-    assert L.kh_block_dots(ctypes.byref(w), k, q.ctypes.data, rows, dots.ctypes.data,
-                           ws.ctypes.data, ws.size, None) == 0
-    report(f"dots fmt {fmt}/{group} rows {rows}", bool(np.array_equal(dots, dots_cpu)))
+    if dots:
+        dots = np.zeros((rows, n, k // 16), np.int32)
+        assert L.kh_block_dots(ctypes.byref(w), k, q.ctypes.data, rows, dots.ctypes.data,
+                               ws.ctypes.data, ws.size, None) == 0
+        report(f"dots fmt {fmt}/{group} rows {rows}", bool(np.array_equal(dots, dots_cpu)))
     got = product([(fmt, group, d, n)], k, x, flags=1).astype(np.float64)
     dense = ko.dequantize(fmt, group, d).reshape(n, k)
     xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
@@ -220,7 +221,20 @@ def main(which):
         case_bytes(fmt, group, 13, 1024, 1 if which == "quick" else 6)
     case_bytes(Q6K, 0, 40, 4096, 16)        # byte activations, 16 rows, four chunks
     case_bytes(Q4K, 0, 20, 512, 40)         # byte activations, 40 rows: three row chunks
-    case_product(Q4_0, 0, 24, 256, 19)      # f32 activations, 19 rows: three row chunks
+    case_product(Q4_0, 0, 24, 256, 19)      # f32 activations, 19 rows: the many-row product
+    # The many-row product: partial column groups and row tiles, K splits,
+    # units past K, stacked weights of one format.
+    case_product(Q4K, 0, 300, 1024, 40)     # three planes, two row tiles, two K splits
+    case_bytes(Q8_0, 0, 270, 1024, 70, dots=False)  # bytes, 64-row tiles, units past K: no
+    case_bytes(Q6K, 0, 40, 512, 33, dots=False)     # groups of 16
+    case_product(Q2K, 0, 30, 512, 20)       # groups of 16 with minimums
+    case_product(Q4_0, 0, 20, 96, 33)       # a unit past K (96 = 3 blocks)
+    case_product(Q5_1, 0, 20, 160, 9)       # minimums of the 32-element blocks
+    case_bytes(INT4, 32, 20, 160, 24, dots=False)
+    k = 512
+    parts = [(Q4K, 0, blocks(Q4K, 0, n * k // 256, 60 + i), n) for i, n in enumerate((260, 7))]
+    x = xs(21, k, 5)
+    check_f32("stacked many-row", product(parts, k, x), ko.product_f64(parts, k, x))
     if which == "all":
         for fmt, group in FORMATS:
             for rows in (3, 17):

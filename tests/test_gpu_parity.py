@@ -305,3 +305,81 @@ def test_low_bit_mix_and_output_table_sample(hip):
             sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
             e64 = ko.product_f64([(fmt, group, sub, len(sample))], k, x)
             check_f32(got[:, sample], e64, f"fmt {fmt} rows {rows}")
+
+
+# ------------------------------------------------------------ many rows
+
+def exact_bytes(fmt, group, data, n, k, x):
+    """The exact product of the quantized activations (bytes.rs:144-158) and
+    the dequantized weights, and the size bound sum |x_q w|."""
+    q, s, _ = ko.quantize_x(x)
+    dense = ko.dequantize(fmt, group, data).reshape(n, k)
+    xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+    return xq @ dense.T, np.abs(xq) @ np.abs(dense).T
+
+
+@pytest.mark.parametrize("fmt,group", FORMATS)
+def test_many_rows_of_every_format(hip, fmt, group):
+    """The many-row product (M > 16): 40 and 130 activation rows by 300
+    weight rows (a partial column group, partial row tiles, splits of K),
+    f32 activations against the f64 product, bytes against the exact product
+    of the quantized activations; bitwise equal on a second run."""
+    k, n = 1280, 300
+    data, w = weight(fmt, group, n, k, 70 + fmt, hip)
+    byte = (fmt, group) in BYTE_FORMATS
+    for rows in (40, 130):
+        x = x_uniform(rows, k, 300 + rows)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        check_f32(got, ko.product_f64([(fmt, group, data, n)], k, x), f"fmt {fmt}/{group} rows {rows}")
+        again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        if byte:
+            hip.with_byte_activations(True)
+            try:
+                got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy().astype(np.float64)
+            finally:
+                hip.with_byte_activations(False)
+            e, size = exact_bytes(fmt, group, data, n, k, x)
+            assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6), f"bytes fmt {fmt}/{group} rows {rows}"
+
+
+QWEN3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+            ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
+
+
+def test_qwen3_8b_prefill_at_full_size(hip):
+    """Config 4: the Q8_0 layer of Qwen3-8B at M = 512 with bf16 activations
+    and byte activations, each stacked call at full size.  A sample of 64
+    weight rows of each matrix is checked on the first and last 8 activation
+    rows against the CPU algorithm (bytes.rs:200-241); every output is
+    finite and a second run is bitwise equal."""
+    rows = 512
+    hip.with_byte_activations(True)
+    try:
+        mats = {name: synth_weight(ka.Q8_0, 0, n, k, 3000 + i) + (n, k)
+                for i, (name, n, k) in enumerate(QWEN3_8B)}
+        for call in (("q", "k", "v"), ("o",), ("gate", "up"), ("down",)):
+            k = mats[call[0]][3]
+            xb = dev(synth.normal(11, rows * k, 1.0).reshape(rows, k), torch.bfloat16)
+            ws = [mats[c][1] for c in call]
+            got = hip.forward(ka.QuantizedMatmul(), [xb] + ws)
+            again = hip.forward(ka.QuantizedMatmul(), [xb] + ws)
+            got = got.float().cpu().numpy()
+            assert np.isfinite(got).all()
+            assert np.array_equal(got, again.float().cpu().numpy())
+            x = xb.float().cpu().numpy()
+            pick = np.r_[0:8, rows - 8:rows]
+            col = 0
+            for c in call:
+                data, _, n, kk = mats[c]
+                sample = np.linspace(0, n - 1, 64).astype(int)
+                rb = ko.row_bytes(ka.Q8_0, 0, kk)
+                sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
+                want = ko.product_bytes([(ka.Q8_0, 0, sub, len(sample))], kk, x[pick])
+                e, size = exact_bytes(ka.Q8_0, 0, sub, len(sample), kk, x[pick])
+                have = got[pick][:, col + sample].astype(np.float64)
+                # bf16 output: within its rounding of the CPU's f32 result.
+                assert np.all(np.abs(have - want) <= 2 ** -8 * np.abs(want) + 2e-5 * size + 2e-6), c
+                col += n
+    finally:
+        hip.with_byte_activations(False)
