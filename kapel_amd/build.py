@@ -17,6 +17,9 @@ ARCH = "gfx950"
 HIP_FLAGS = ["--offload-arch=" + ARCH, "-O3", "-fPIC", "-std=c++17",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-ffp-contract=off", "-Wno-unused-command-line-argument"]
+# The many-row product's MFMA results go to VGPRs, where its VALU work reads
+# them, rather than to AGPRs (a copy per element).
+MM_FLAGS = ["-mllvm", "-amdgpu-mfma-vgpr-form"]
 HOST_FLAGS = ["-O3", "-fPIC", "-std=c++17", "-ffp-contract=off", "-fno-fast-math"]
 
 
@@ -37,9 +40,9 @@ def build(verbose=False):
         ("kh_gemv_b.hip", HIPCC, HIP_FLAGS),
         ("kh_gemv_i.hip", HIPCC, HIP_FLAGS),
         ("kh_mm.hip", HIPCC, HIP_FLAGS),
-        ("kh_mm_k.hip", HIPCC, HIP_FLAGS),
-        ("kh_mm_b.hip", HIPCC, HIP_FLAGS),
-        ("kh_mm_i.hip", HIPCC, HIP_FLAGS),
+        ("kh_mm_k.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
+        ("kh_mm_b.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
+        ("kh_mm_i.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_api.cpp", HIPCC, HIP_FLAGS),
         ("kh_quantize.cpp", "g++", HOST_FLAGS),
     )

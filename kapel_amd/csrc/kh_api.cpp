@@ -122,26 +122,39 @@ GemvSplit gemv_split(uint64_t k, int unit, int tiles, int rows, int planes, int 
     return g;
 }
 
-// The many-row product's split, a function of the shapes only: 64 activation
-// rows a workgroup with bytes (32 with three planes), column groups of 256
-// weight rows, and K split into `ks` ranges of `ups` units when the row and
-// column tiles give fewer than 256 workgroups (one a CU: a workgroup fills its
-// CU's registers).  Each range keeps at least 512 elements of K.
+// The many-row product's split, a function of the shapes only: the kernel's
+// row tiles (mm_shape), its column groups (mm_cols), and K split into `ks`
+// ranges of `ups` units when that shortens the rounds of 256 workgroups (one
+// a CU: a workgroup fills its CU's LDS).  Each range keeps at least 512
+// elements of K.
 struct MmSplit {
-    int wm, mtiles, ngroups, units, ups, ks;
+    int wm, wmg, cols, mtiles, ngroups, units, ups, ks;
 };
 
-constexpr int MM_COLS = 256;
-
-MmSplit mm_split(uint64_t rows, uint64_t k, int unit, int planes, int ngroups) {
+MmSplit mm_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std::vector<uint32_t> &members,
+                 int planes) {
+    const kh_weight &w = weights[members[0]];
     MmSplit m{};
-    m.wm = planes == 1 && rows > 32 ? 2 : 1;
-    m.mtiles = (int)div_up(rows, 32 * m.wm);
-    m.ngroups = ngroups;
+    mm_shape(planes, (int)rows, m.wm, m.wmg);
+    m.cols = mm_cols(w.format, w.group, planes, (int)rows);
+    m.mtiles = (int)div_up(rows, 32 * m.wm * m.wmg);
+    m.ngroups = 0;
+    for (uint32_t i : members) m.ngroups += (int)div_up(weights[i].n, m.cols);
+    const int unit = mm_unit(w.format, w.group);
     m.units = (int)div_up(k, unit);
-    uint64_t base = (uint64_t)m.mtiles * ngroups;
+    // The time of a split: rounds of 256 workgroups times units each; a
+    // split is taken when it saves more than 15 % (its partial sums cost a
+    // pass of their own).
+    uint64_t base = (uint64_t)m.mtiles * m.ngroups;
     int most = std::max(1, m.units / (int)div_up(512, unit));
-    int ks = (int)std::min<uint64_t>(most, std::max<uint64_t>(1, div_up(256, base)));
+    auto cost = [&](int ks) { return div_up(base * ks, 256) * div_up(m.units, ks); };
+    int ks = 1;
+    uint64_t best = cost(1);
+    for (int s = 2; s <= most; s++)
+        if (cost(s) * 100 < best * 85) {
+            ks = s;
+            best = cost(s);
+        }
     m.ups = (int)div_up(m.units, ks);
     m.ks = (int)div_up(m.units, m.ups);
     return m;
@@ -246,12 +259,10 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
             L.mm = true;
             uint64_t kpad = align_up(std::max<uint64_t>(k, 64), 64);
             uint64_t fit = ((1ull << 31) - 1) / ((uint64_t)planes * kpad) / 64 * 64;
-            int ngroups = 0;
-            for (uint32_t m : L.members) ngroups += (int)div_up(weights[m].n, MM_COLS);
             for (uint64_t r0 = 0; r0 < rows; r0 += fit) {
                 L.r0 = r0;
                 L.rows = (int)std::min<uint64_t>(fit, rows - r0);
-                L.msplit = mm_split((uint64_t)L.rows, k, unit, planes, ngroups);
+                L.msplit = mm_split((uint64_t)L.rows, k, weights, L.members, planes);
                 fn(L);
             }
             continue;
@@ -431,7 +442,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
                 a.n[m] = wm.n;
                 a.col0[m] = col0[L.members[m]];
                 a.ng0[m] = ng;
-                ng += (int)div_up(wm.n, MM_COLS);
+                ng += (int)div_up(wm.n, L.msplit.cols);
             }
             uint32_t len = kh_block_len(w.format, w.group), size = kh_block_bytes(w.format, w.group);
             const int g = mm_group(w.format, w.group);
@@ -443,6 +454,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.ngroups = L.msplit.ngroups;
             a.mtiles = L.msplit.mtiles;
             a.wm = L.msplit.wm;
+            a.wmg = L.msplit.wmg;
             a.rows = L.rows;
             const uint64_t r0 = L.r0;
             a.planes = reinterpret_cast<const int8_t *>(ws + l.planes_off) + r0 * planes * l.kpad;

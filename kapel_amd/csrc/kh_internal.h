@@ -107,8 +107,8 @@ struct GemvArgs {
 };
 
 // The many-row product (kh_mm.h): weights of one format in column groups of
-// 256 rows; a workgroup takes one group, 32 or 64 activation rows (`wm`
-// tiles of 32) and one of `ks` splits of K (`ups` units each).
+// 256 (or 128) rows; a workgroup takes one group, wmg x wm x 32 activation
+// rows and one of `ks` splits of K (`ups` units each).
 struct MmArgs {
     int count;
     const uint8_t *w[MAX_WEIGHTS];
@@ -117,7 +117,8 @@ struct MmArgs {
     uint64_t col0[MAX_WEIGHTS];
     int ng0[MAX_WEIGHTS];          // first column group of each weight
     uint64_t row_bytes;
-    int k, units, ups, ks, ngroups, mtiles, wm;
+    int k, units, ups, ks, ngroups, mtiles;
+    int wm, wmg;                   // row tiles of 32 a wave, groups of waves a workgroup
     int rows;                      // activation rows of this launch
     // Prepared activations of these rows (prep_x_kernel).
     const int8_t *planes;          // [rows][P][kpad]
@@ -168,6 +169,12 @@ hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs 
 // The many-row product: the size of a format's scale groups (32 or 16; 0:
 // not read by it).
 int mm_group(uint32_t fmt, uint32_t group);
+// Elements of K a unit of it takes, and the weight rows of its column
+// groups (for `wm` row tiles of 32).
+int mm_unit(uint32_t fmt, uint32_t group);
+int mm_cols(uint32_t fmt, uint32_t group, int planes, int rows);
+// Row tiles of a wave and groups of waves of a workgroup for `rows` rows.
+void mm_shape(int planes, int rows, int &wm, int &wmg);
 hipError_t launch_mm(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s);
 hipError_t launch_mm_reduce(const MmArgs &a, hipStream_t s);
 hipError_t launch_generic(const GenericArgs &a, hipStream_t s);

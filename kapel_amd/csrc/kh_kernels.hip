@@ -55,80 +55,137 @@ __device__ __forceinline__ void store_out(uint32_t kind, void *out, uint64_t i, 
 }
 
 // --------------------------------------------------------------- prep_x
-// One thread per element; a half-wave (32 lanes) per block of 32.  Writes the
-// planes [rows][planes][kpad], xscale [rows][k/32], the sums of each group of
-// 16 and 32 as floats (x's value: xsum = xscale * sum of the plane values)
-// and of 16 as integers.
+// Eight consecutive elements a thread, four threads (consecutive lanes) a
+// block of 32.  Writes the planes [rows][planes][kpad], xscale [rows][k/32],
+// the sums of each group of 16 and 32 as floats (x's value: xsum = xscale *
+// sum of the plane values) and of 16 as integers.
+constexpr int PREP_E = 8;
+
+__device__ __forceinline__ void load8(uint32_t kind, const void *x, uint64_t e, bool vec, float (&v)[PREP_E]) {
+    if (vec && kind == KH_F32) {
+        const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(x) + e);
+        float4 a = p[0], b = p[1];
+        v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+    } else if (vec) {
+        uint4 w = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(x) + e);
+        uint32_t d[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            uint32_t lo = d[i] & 0xffffu, hi = d[i] >> 16;
+            v[2 * i] = kind == KH_BF16 ? __uint_as_float(lo << 16) : h2f(lo);
+            v[2 * i + 1] = kind == KH_BF16 ? __uint_as_float(hi << 16) : h2f(hi);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) v[i] = load_x(kind, x, e + i);
+    }
+}
+
 __global__ __launch_bounds__(256) void prep_x_kernel(PrepArgs a) {
-    uint64_t e = (uint64_t)blockIdx.x * 256 + threadIdx.x;
-    uint64_t total = a.rows * a.k;
-    bool live = e < total;
-    float v = live && !a.q_in ? load_x(a.x_kind, a.x, e) : 0.0f;
-    uint64_t m = live ? e / a.k : 0, col = live ? e % a.k : 0;
-    float mag = fabsf(v);
-    // f32::max ignores NaN, as fmaxf does: bytes.rs:148-151.
-    float max = mag;
-    for (int s = 1; s < 32; s <<= 1) max = fmaxf(max, __shfl_xor(max, s, 32));
-    int digit[3] = {0, 0, 0};
-    int value;      // the integer this element stands for: q, or x * 2^sh
-    float xscale;   // its weight: element = xscale * value
+    const uint64_t t = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    const uint64_t total = a.rows * a.k / PREP_E;
+    const bool live = t < total;
+    const uint64_t e = live ? t * PREP_E : 0;
+    const uint64_t m = e / a.k, col = e % a.k;
+    // Vector loads when x allows them (rows start at multiples of 32
+    // elements).
+    const bool vec = ((uintptr_t)a.x & 15u) == 0;
+    float v[PREP_E];
+    if (a.q_in || !live) {
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) v[i] = 0.0f;
+    } else {
+        load8(a.x_kind, a.x, e, vec, v);
+    }
+    float mag[PREP_E], max = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PREP_E; i++) {
+        mag[i] = fabsf(v[i]);
+        // f32::max ignores NaN, as fmaxf does: bytes.rs:148-151.
+        max = fmaxf(max, mag[i]);
+    }
+    max = fmaxf(max, __shfl_xor(max, 1));
+    max = fmaxf(max, __shfl_xor(max, 2));
+    int value[PREP_E];  // the integers these elements stand for: q, or x * 2^sh
+    int digit[3][PREP_E];
+    float xscale;      // their weight: element = xscale * value
     if (a.q_in) {
         // Bytes given (kh_block_dots): only their sums are wanted.
         xscale = 1.0f;
-        value = digit[0] = live ? (int)a.q_in[e] : 0;
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) value[i] = digit[0][i] = live ? (int)a.q_in[e + i] : 0;
     } else if (a.planes == 1) {
         // bytes.rs:152-156: s = max / 127 (correctly rounded division),
         // q = round-half-even(x * (127 / max)) clamped to +-127; NaN -> 0.
         xscale = max / 127.0f;
-        float inverse = max > 0.0f ? 127.0f / max : 0.0f;
-        float r = rintf(v * inverse);
-        r = r != r ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
-        value = digit[0] = (int)r;
+        const float inverse = max > 0.0f ? 127.0f / max : 0.0f;
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) {
+            float r = rintf(v[i] * inverse);
+            r = r != r ? 0.0f : fminf(fmaxf(r, -127.0f), 127.0f);
+            value[i] = digit[0][i] = (int)r;
+        }
     } else {
         // 23-bit fixed point against the block's largest magnitude, in three
         // signed bytes: value = d0 * 2^16 + d1 * 2^8 + d2, |value| <= 2^22,
         // |d0| <= 64.
-        bool finite = isfinite(max);
+        const bool finite = isfinite(max);
         int exponent = 0;
         if (max > 0.0f && finite) frexpf(max, &exponent);  // max < 2^exponent
-        int sh = 22 - exponent;
-        float f = (max > 0.0f && finite) ? rintf(__builtin_ldexpf(v, sh)) : 0.0f;
-        value = f != f ? 0 : (int)f;
-        int c = ((value + 128) & 255) - 128;
-        int r1 = (value - c) >> 8;
-        int b = ((r1 + 128) & 255) - 128;
-        digit[0] = (r1 - b) >> 8;
-        digit[1] = b;
-        digit[2] = c;
+        const int sh = 22 - exponent;
+        int bad = 0;
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) {
+            const float f = (max > 0.0f && finite) ? rintf(__builtin_ldexpf(v[i], sh)) : 0.0f;
+            value[i] = f != f ? 0 : (int)f;
+            const int c = ((value[i] + 128) & 255) - 128;
+            const int r1 = (value[i] - c) >> 8;
+            const int b = ((r1 + 128) & 255) - 128;
+            digit[0][i] = (r1 - b) >> 8;
+            digit[1][i] = b;
+            digit[2][i] = c;
+            bad |= (!finite || mag[i] != mag[i]) ? 1 : 0;
+        }
         // A block holding a NaN or an infinity gives NaN, as the product does.
-        int bad = (!finite || mag != mag) ? 1 : 0;
-        for (int s = 1; s < 32; s <<= 1) bad |= __shfl_xor(bad, s, 32);
-        xscale = bad ? __uint_as_float(0x7fc00000u)
-                     : (max > 0.0f ? __builtin_ldexpf(1.0f, -sh) : 0.0f);
+        bad |= __shfl_xor(bad, 1);
+        bad |= __shfl_xor(bad, 2);
+        xscale = bad ? __uint_as_float(0x7fc00000u) : (max > 0.0f ? __builtin_ldexpf(1.0f, -sh) : 0.0f);
     }
-    int v16 = value;
-    for (int s = 1; s < 16; s <<= 1) v16 += __shfl_xor(v16, s, 32);
-    int other = __shfl_xor(v16, 16, 32);
+    int v8 = 0;
+#pragma unroll
+    for (int i = 0; i < PREP_E; i++) v8 += value[i];
+    const int v16 = v8 + __shfl_xor(v8, 1);
+    const int other = __shfl_xor(v16, 2);
     if (!live) return;
-    uint64_t blk32 = m * (a.k / 32) + col / 32;
-    uint64_t g16 = m * (a.k / 16) + col / 16;
-    int lane32 = (int)(col % 32);
-    if (lane32 == 0 || lane32 == 16) {
+    const int quarter = (int)(col % 32) / PREP_E;
+    const uint64_t blk32 = m * (a.k / 32) + col / 32;
+    const uint64_t g16 = m * (a.k / 16) + col / 16;
+    if ((quarter & 1) == 0) {
         if (a.xsumi16) a.xsumi16[g16] = v16;
         if (a.xsum16) a.xsum16[g16] = xscale * (float)v16;
     }
-    if (lane32 == 0) {
+    if (quarter == 0) {
         // bytes.rs:126-128: scale * (sum of the block's q as i32) as f32.
-        float sum32 = xscale * (float)(v16 + other);
+        const float sum32 = xscale * (float)(v16 + other);
         if (a.xscale) a.xscale[blk32] = xscale;
         if (a.xsum32) a.xsum32[blk32] = sum32;
         if (a.q_scale) a.q_scale[blk32] = xscale;
         if (a.q_sums) a.q_sums[blk32] = sum32;
     }
+    auto pack = [&](const int (&d)[PREP_E]) {
+        uint2 w;
+        w.x = (uint32_t)(d[0] & 0xff) | (uint32_t)(d[1] & 0xff) << 8 | (uint32_t)(d[2] & 0xff) << 16 |
+              (uint32_t)(d[3] & 0xff) << 24;
+        w.y = (uint32_t)(d[4] & 0xff) | (uint32_t)(d[5] & 0xff) << 8 | (uint32_t)(d[6] & 0xff) << 16 |
+              (uint32_t)(d[7] & 0xff) << 24;
+        return w;
+    };
     if (a.planes_out)
         for (int p = 0; p < a.planes; p++)
-            a.planes_out[(m * a.planes + p) * a.kpad + col] = (int8_t)digit[p];
-    if (a.q_out) a.q_out[e] = (int8_t)digit[0];
+            *reinterpret_cast<uint2 *>(a.planes_out + (m * a.planes + p) * a.kpad + col) = pack(digit[p]);
+    if (a.q_out)
+#pragma unroll
+        for (int i = 0; i < PREP_E; i++) a.q_out[e + i] = (int8_t)digit[0][i];
 }
 
 // Zero-fills `words` u32 (a graph-safe replacement for a memset).
@@ -530,7 +587,7 @@ hipError_t launch_qmv(uint32_t fmt, uint32_t group, int planes, const QmvArgs &a
 }
 
 hipError_t launch_prep(const PrepArgs &a, hipStream_t s) {
-    uint64_t total = a.rows * a.k;
+    uint64_t total = a.rows * a.k / PREP_E;
     if (total == 0) return hipSuccess;
     hipLaunchKernelGGL(prep_x_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, a);
     return hipGetLastError();

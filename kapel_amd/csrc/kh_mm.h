@@ -71,24 +71,41 @@ __device__ __forceinline__ uint32_t sub_bytes(uint32_t x, uint32_t o) {
 }
 __device__ __forceinline__ uint64_t pair(uint32_t lo, uint32_t hi) { return (uint64_t)hi << 32 | lo; }
 
+// The bytes of a workgroup's stage in LDS, read as dwords (offsets a multiple
+// of 4 for ld, of 2 for rn).
+struct Lds {
+    const uint8_t *p;
+};
+
 template <int N>
-__device__ __forceinline__ void ld(uint32_t (&v)[N], const Src &s, uint32_t off) {
-    lanes::ldb<N>(v, s, off);
+__device__ __forceinline__ void ld(uint32_t (&v)[N], const Lds &s, uint32_t off) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(s.p + off);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = w[i];
 }
 template <int R>
-__device__ __forceinline__ void rn(uint32_t (&w)[(R + 3) / 4], const Src &s, uint32_t off) {
-    lanes::run<R>(w, s, off);
+__device__ __forceinline__ void rn(uint32_t (&w)[(R + 3) / 4], const Lds &s, uint32_t off) {
+    static_assert(R % 2 == 0, "even runs only");
+    constexpr int D = (R + 5) / 4, W = (R + 3) / 4;
+    const uint32_t a = off & 2u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(s.p + (off - a));
+    uint32_t v[D + 1];
+#pragma unroll
+    for (int i = 0; i < D; i++) v[i] = p[i];
+    v[D] = 0u;
+#pragma unroll
+    for (int i = 0; i < W; i++) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], a);
 }
 
 // ------------------------------------------------ 256-element super-blocks
 // Q4_K: nibbles of sub-block 2c (low) and 2c + 1 (high) at 16 + 32c + l.
 struct Q4K {
-    static constexpr int U = 256, G = 32, NG = 8, BYTES = 144;
+    static constexpr int U = 256, G = 32, NG = 8, BYTES = 144, BLEN = 256;
     static constexpr bool MIN = true;
     struct Regs {
         uint32_t h[4], q[4][4];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
         ld<4>(r.h, s, b);
 #pragma unroll
@@ -111,12 +128,12 @@ struct Q4K {
 // Q5_K: as Q4_K, fifth bit of element 32j + l in bit j of byte 16 + l,
 // nibbles at 48.
 struct Q5K {
-    static constexpr int U = 256, G = 32, NG = 8, BYTES = 176;
+    static constexpr int U = 256, G = 32, NG = 8, BYTES = 176, BLEN = 256;
     static constexpr bool MIN = true;
     struct Regs {
         uint32_t h[4], qh[4], q[4][4];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
         ld<4>(r.h, s, b);
         ld<4>(r.qh, s, b + 16 + 16 * h);
@@ -141,12 +158,12 @@ struct Q5K {
 // Q6_K (210 bytes): low nibble t / 2 of byte 64a + 32 (t % 2) + l, high bits
 // 2t of byte 128 + 32a + l, signed scales at 192, d at 208; codes - 32.
 struct Q6K {
-    static constexpr int U = 256, G = 16, NG = 16, BYTES = 210;
+    static constexpr int U = 256, G = 16, NG = 16, BYTES = 210, BLEN = 256;
     static constexpr bool MIN = false;
     struct Regs {
         uint32_t ql[8][2], qh[4][2], sc[5];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 8; i++)  // (a, t % 2, j % 2)
@@ -176,12 +193,12 @@ struct Q6K {
 // Q2_K (84 bytes): scale bytes at 0 (low nibble scale, high minimum), codes
 // bits 2t of byte 16 + 32a + l, d and dmin at 80.
 struct Q2K {
-    static constexpr int U = 256, G = 16, NG = 16, BYTES = 84;
+    static constexpr int U = 256, G = 16, NG = 16, BYTES = 84, BLEN = 256;
     static constexpr bool MIN = true;
     struct Regs {
         uint32_t q[4][2], sc[4], dd[1];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 4; i++) ld<2>(r.q[i], s, b + 16 + 32 * (i >> 1) + 16 * (i & 1) + 8 * h);
@@ -207,12 +224,12 @@ struct Q2K {
 // Q3_K (110 bytes): high bit 4a + t of byte l, low bits 2t of byte 32 + 32a
 // + l, 12 bytes of 6-bit scales at 96, d at 108; codes - 4.
 struct Q3K {
-    static constexpr int U = 256, G = 16, NG = 16, BYTES = 110;
+    static constexpr int U = 256, G = 16, NG = 16, BYTES = 110, BLEN = 256;
     static constexpr bool MIN = false;
     struct Regs {
         uint32_t hm[2][2], q[4][2], sc[4];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 2; i++) rn<8>(r.hm[i], s, b + 16 * i + 8 * h);
@@ -249,12 +266,12 @@ struct Q3K {
 
 // Q8_0: d, 32 signed bytes.
 struct Q8_0 {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = 34;
+    static constexpr int U = 128, G = 32, NG = 4, BYTES = 34, BLEN = 32;
     static constexpr bool MIN = false;
     struct Regs {
         uint32_t c[4][4], d[4][1];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t b = row + (4 * u + j) * BYTES;
@@ -283,12 +300,12 @@ __device__ __forceinline__ v4i nibbles(const uint32_t *q, int h, uint32_t offset
 
 // Q4_0: d, 16 bytes (byte i: element i low nibble, i + 16 high); codes - 8.
 struct Q4_0 {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = 18;
+    static constexpr int U = 128, G = 32, NG = 4, BYTES = 18, BLEN = 32;
     static constexpr bool MIN = false;
     struct Regs {
         uint32_t w[4][5];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) rn<18>(r.w[j], s, row + (4 * u + j) * BYTES);
     }
@@ -306,12 +323,12 @@ struct Q4_0 {
 
 // Q4_1: d, m, 16 bytes of nibbles; w = d q + m (minimum -m).
 struct Q4_1 {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = 20;
+    static constexpr int U = 128, G = 32, NG = 4, BYTES = 20, BLEN = 32;
     static constexpr bool MIN = true;
     struct Regs {
         uint32_t w[4][5];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) ld<5>(r.w[j], s, row + (4 * u + j) * BYTES);
     }
@@ -329,12 +346,12 @@ struct Q4_1 {
 // Q5_1: d, m, fifth bits, nibbles; w = d q + m.
 template <bool ONE>
 struct Q5x {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = ONE ? 24 : 22;
+    static constexpr int U = 128, G = 32, NG = 4, BYTES = ONE ? 24 : 22, BLEN = 32;
     static constexpr bool MIN = ONE;
     struct Regs {
         uint32_t w[4][6];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t b = row + (4 * u + j) * BYTES;
@@ -373,18 +390,19 @@ struct Q5x {
 
 // Kapel int8 / int4 in groups of GR (a multiple of 32): an f32 scale, then GR
 // bytes, or GR / 2 bytes of nibbles (element 2i low, 2i + 1 high); int4
-// codes - 8.  Group j of unit u is the piece of 32 elements p = 4u + j.
+// codes - 8.  A unit is 128 elements, or one group of 256; group j of unit
+// u is the piece of 32 elements p = NG u + j.
 template <int GR>
 struct Int8G {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = 4 + GR;
+    static constexpr int U = GR > 128 ? GR : 128, G = 32, NG = U / 32, BYTES = 4 + GR, BLEN = GR;
     static constexpr bool MIN = false;
     struct Regs {
-        uint32_t c[4][4], sc[4][1];
+        uint32_t c[NG][4], sc[NG][1];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int p = 4 * u + j;
+        for (int j = 0; j < NG; j++) {
+            const int p = NG * u + j;
             const uint32_t b = row + (uint32_t)(32 * p / GR) * BYTES;
             ld<1>(r.sc[j], s, b);
             ld<4>(r.c[j], s, b + 4 + (32 * p) % GR + 16 * h);
@@ -395,21 +413,21 @@ struct Int8G {
     }
     __device__ static void scales(const Regs &r, float (&sc)[NG], float (&)[NG]) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) sc[j] = __uint_as_float(r.sc[j][0]);
+        for (int j = 0; j < NG; j++) sc[j] = __uint_as_float(r.sc[j][0]);
     }
 };
 
 template <int GR>
 struct Int4G {
-    static constexpr int U = 128, G = 32, NG = 4, BYTES = 4 + GR / 2;
+    static constexpr int U = GR > 128 ? GR : 128, G = 32, NG = U / 32, BYTES = 4 + GR / 2, BLEN = GR;
     static constexpr bool MIN = false;
     struct Regs {
-        uint32_t c[4][2], sc[4][1];
+        uint32_t c[NG][2], sc[NG][1];
     };
-    __device__ static void load(Regs &r, const Src &s, uint32_t row, int u, int h) {
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int p = 4 * u + j;
+        for (int j = 0; j < NG; j++) {
+            const int p = NG * u + j;
             const uint32_t b = row + (uint32_t)(32 * p / GR) * BYTES;
             ld<1>(r.sc[j], s, b);
             ld<2>(r.c[j], s, b + 4 + ((32 * p) % GR) / 2 + 8 * h);
@@ -427,31 +445,64 @@ struct Int4G {
     }
     __device__ static void scales(const Regs &r, float (&sc)[NG], float (&)[NG]) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) sc[j] = __uint_as_float(r.sc[j][0]);
+        for (int j = 0; j < NG; j++) sc[j] = __uint_as_float(r.sc[j][0]);
     }
 };
 
 // ---------------------------------------------------------- the kernel
-constexpr int WAVES = 4;         // waves of a workgroup
-constexpr int WN = 2;            // weight tiles of 32 rows a wave
-constexpr int NCOLS = WAVES * WN * 32;  // weight rows of a workgroup
+constexpr int LDS_MAX = 160 * 1024;      // LDS of a CU (gfx950)
 
-// Bytes of one row of a staged plane: the unit plus a pad that spreads the
-// rows of an LDS read over all banks.
-template <class F>
-constexpr int row_stride() { return F::U + (F::G == 32 ? 16 : 8); }
+// The LDS stage of one unit, filled by direct loads to LDS (each wave
+// instruction writes 64 lanes x 16 bytes, or x 4 bytes, consecutive): the
+// activation rows [P][RM] of the unit's U bytes (16-byte chunks in a
+// swizzled order: chunk o of row r at o ^ swz(r), so that an LDS read of one
+// chunk by 16 rows touches every bank once), the weight rows [NCOLS] of CW
+// chunks (the unit's UB bytes from the dword at or below their start), the
+// activation scales [RM][U / 32] and sums [RM][U / G].  Every region is a
+// whole number of instructions for each wave.  A workgroup is WMG x 4 waves:
+// WMG groups of WM row tiles of 32, by 4 x WN weight tiles of 32.
+template <class F, int P, int WM, int WMG, int WN>
+struct Plan {
+    static constexpr int WAVES = 4 * WMG;
+    static constexpr int U = F::U, G = F::G, RM = 32 * WM * WMG, NS = U / 32, NX = U / G;
+    static constexpr int UB = U / F::BLEN * F::BYTES;
+    static constexpr bool ODD = F::BYTES % 4 != 0;  // blocks at even offsets
+    static constexpr int CW = (UB + (ODD ? 2 : 0) + 15) / 16;
+    static constexpr int AW = U / 16;
+    static constexpr int NCOLS = 4 * WN * 32;
+    static constexpr int up(int x) { return (x + WAVES - 1) / WAVES * WAVES; }
+    static constexpr int IA = up((P * RM * AW + 63) / 64);
+    static constexpr int IW = up((NCOLS * CW + 63) / 64);
+    static constexpr int IS = up((RM * NS + 63) / 64);
+    static constexpr int IX = F::MIN ? up((RM * NX + 63) / 64) : 0;
+    static constexpr int OA = 0, OW = IA * 1024, OS = OW + IW * 1024, OX = OS + IS * 256;
+    static constexpr int SB = OX + IX * 256;
+    static constexpr int D = (IA + IW + IS + IX) / WAVES;  // instructions a wave issues a stage
+    static constexpr int STAGES = 3 * SB <= LDS_MAX ? 3 : 2;
+    static constexpr bool FITS = 2 * SB <= LDS_MAX;
+    static_assert(D * (STAGES - 2) <= 63, "the later stages' loads fit vmcnt");
+    // The position of chunk o of activation row r.
+    static constexpr int swz(int r) { return U == 128 ? (r >> 1) & 7 : r & 15; }
+};
 
-// LDS bytes of one stage buffer: planes [P][RM][stride], scales [U/32][RM],
-// sums [U/G][RM] (MIN).
-template <class F, int P, int RM>
-constexpr int stage_bytes() {
-    return P * RM * row_stride<F>() + (F::U / 32) * RM * 4 + (F::MIN ? (F::U / F::G) * RM * 4 : 0);
+// Weight tiles of a wave: two, or one for the formats with a minimum term or
+// more than 24 dwords of a unit's lane bytes (their registers would not fit
+// two waves a SIMD) and where two stages of two would not fit in LDS.
+template <class F, int P, int WM, int WMG>
+constexpr int wn_of() {
+    return !F::MIN && sizeof(typename F::Regs) <= 96 && Plan<F, P, WM, WMG, 2>::FITS ? 2 : 1;
 }
 
 // An empty asm through which a value must pass (its order among the others
 // is kept).
 #ifndef KH_PIN
 #define KH_PIN(x) asm volatile("" : "+v"(x))
+#endif
+// A direct load to LDS: `size` bytes of each lane at buffer offset voff, to
+// lds + size * lane.
+#ifndef KH_LDS_LOAD
+#define KH_LDS_LOAD(rsrc, lds, size, voff) \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds((rsrc), (__attribute__((address_space(3))) void *)(lds), (size), (int)(voff), 0, 0, 0)
 #endif
 
 __device__ __forceinline__ v16i mfma_dot(v4i a, v4i b) {
@@ -461,16 +512,20 @@ __device__ __forceinline__ v16i mfma_dot(uint64_t a, uint64_t b) {
     return __builtin_amdgcn_mfma_i32_32x32x16_i8((long)a, (long)b, v16i{}, 0, 0, 0);
 }
 
-template <class F, int P, int WM>
-__global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
-    constexpr int U = F::U, G = F::G, NG = F::NG, RM = WM * 32;
-    constexpr int RS = row_stride<F>(), NS = U / 32, NX = U / G;
-    constexpr int T = 64 * WAVES;
-    constexpr int CC = P * RM * U / 16;            // 16-byte pieces of a stage
-    constexpr int CPT = (CC + T - 1) / T;
-    constexpr int SPT = (RM * NS + T - 1) / T;
-    constexpr int XPT = F::MIN ? (RM * NX + T - 1) / T : 0;
-    constexpr int SB = stage_bytes<F, P, RM>();
+// s_waitcnt with vmcnt <= n (and no outstanding LDS work).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+    static_assert(N >= 0 && N <= 63, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
+template <class F, int P, int WM, int WMG>
+__global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
+    constexpr int WN = wn_of<F, P, WM, WMG>();
+    using L = Plan<F, P, WM, WMG, WN>;
+    constexpr int WAVES = L::WAVES;
+    constexpr int U = F::U, G = F::G, NG = F::NG, RM = L::RM, NS = L::NS, NX = L::NX;
+    constexpr int S = L::STAGES, AW = L::AW, CW = L::CW;
     using CodeT = decltype(F::codes(*(const typename F::Regs *)nullptr, 0, 0));
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -486,78 +541,78 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
 
     const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wr = (wave >> 2) * WM * 32;  // this wave's first activation row in the stage
+    const int wc = (wave & 3) * WN * 32;   // and first weight row
     int mat = 0;
     for (int i = 1; i < a.count; i++)
         if (ng >= a.ng0[i]) mat = i;
-    const int64_t n0 = (int64_t)(ng - a.ng0[mat]) * NCOLS + wave * WN * 32;
-    const Src src = lanes::source(a.w[mat], a.wbytes[mat]);
-    uint32_t ro[WN];
-#pragma unroll
-    for (int t = 0; t < WN; t++) {
-        const int64_t n = n0 + t * 32 + c;
-        ro[t] = n < (int64_t)a.n[mat] ? (uint32_t)n * (uint32_t)a.row_bytes : NONE;
-    }
+    const int64_t g0 = (int64_t)(ng - a.ng0[mat]) * L::NCOLS;  // first weight row of the group
+    const int64_t nmat = (int64_t)a.n[mat];
+    const uint32_t row_bytes = (uint32_t)a.row_bytes;
 
-    // Staging of the activations of a unit: every thread loads its pieces
-    // (zeros past the rows or K), then stores them to a stage buffer.
+    // What each lane loads into a stage, by instruction: the offset of its
+    // piece for unit 0 (or NONE) and what moves with the unit.
+    const Src wsrc = lanes::source(a.w[mat], a.wbytes[mat]);
     const Src psrc = lanes::source(a.planes, a.planes_bytes);
     const Src ssrc = lanes::source(a.xscale, (uint32_t)(a.rows * (a.k / 32) * 4));
     const Src xsrc = lanes::source(a.xsum, (uint32_t)(a.rows * (a.k / G) * 4));
-    struct Stage {
-        lanes::u32x4 c[CPT];
-        uint32_t s[SPT];
-        uint32_t x[XPT > 0 ? XPT : 1];
-    };
-    auto stage_load = [&](Stage &st, int u) __attribute__((always_inline)) {
+    constexpr int DA = L::IA / WAVES, DW = L::IW / WAVES, DS = L::IS / WAVES, DX = L::IX / WAVES;
+    uint32_t a_base[DA], a_col[DA], w_row[DW], w_piece[DW], s_base[DS], s_j[DS];
+    uint32_t x_base[DX > 0 ? DX : 1], x_j[DX > 0 ? DX : 1];
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int ci = threadIdx.x + i * T;
-            const int o = ci % (U / 16), rp = ci / (U / 16), r = rp % RM, p = rp / RM;
-            const bool on = ci < CC && m0 + r < a.rows && u * U + 16 * o < a.k;
-            const uint32_t off = on ? (uint32_t)(((m0 + r) * P + p) * a.kpad + u * U + 16 * o) : NONE;
-            st.c[i] = __builtin_amdgcn_raw_buffer_load_b128(psrc.r, (int)off, 0, 0);
+    for (int i = 0; i < DA; i++) {
+        const int ci = (i * WAVES + wave) * 64 + lane, pr = ci / AW, o = (ci % AW) ^ L::swz(pr % RM);
+        const int p = pr / RM, r = pr % RM;
+        const bool on = ci < P * RM * AW && m0 + r < a.rows;
+        a_base[i] = on ? (uint32_t)(((uint64_t)(m0 + r) * P + p) * a.kpad + 16 * o) : NONE;
+        a_col[i] = 16 * o;
+    }
+#pragma unroll
+    for (int i = 0; i < DW; i++) {
+        const int ci = (i * WAVES + wave) * 64 + lane, col = ci / CW;
+        const int64_t n = g0 + col;
+        w_row[i] = ci < L::NCOLS * CW && n < nmat ? (uint32_t)n * row_bytes : NONE;
+        w_piece[i] = 16 * (ci % CW);
+    }
+#pragma unroll
+    for (int i = 0; i < DS; i++) {
+        const int di = (i * WAVES + wave) * 64 + lane, r = di / NS;
+        const bool on = di < RM * NS && m0 + r < a.rows;
+        s_base[i] = on ? (uint32_t)(((uint64_t)(m0 + r) * (a.k / 32) + di % NS) * 4) : NONE;
+        s_j[i] = di % NS;
+    }
+#pragma unroll
+    for (int i = 0; i < DX; i++) {
+        const int di = (i * WAVES + wave) * 64 + lane, r = di / NX;
+        const bool on = di < RM * NX && m0 + r < a.rows;
+        x_base[i] = on ? (uint32_t)(((uint64_t)(m0 + r) * (a.k / G) + di % NX) * 4) : NONE;
+        x_j[i] = di % NX;
+    }
+    // The loads of unit u into stage buffer `slot` (units past the range
+    // load nothing: NONE, zeros written, no memory read), D instructions.
+    auto issue = [&](int u, int slot) __attribute__((always_inline)) {
+        uint8_t *st = lds + slot * L::SB;
+        const bool on = u < u1;
+#pragma unroll
+        for (int i = 0; i < DA; i++) {
+            const bool in = on && a_base[i] != NONE && u * U + (int)a_col[i] < a.k;
+            KH_LDS_LOAD(psrc.r, st + L::OA + (i * WAVES + wave) * 1024, 16, in ? a_base[i] + u * U : NONE);
         }
 #pragma unroll
-        for (int i = 0; i < SPT; i++) {
-            const int ci = threadIdx.x + i * T, j = ci % NS, r = ci / NS;
-            const bool on = ci < RM * NS && m0 + r < a.rows && u * NS + j < a.k / 32;
-            const uint32_t off = on ? (uint32_t)(((m0 + r) * (a.k / 32) + u * NS + j) * 4) : NONE;
-            st.s[i] = __builtin_amdgcn_raw_buffer_load_b32(ssrc.r, (int)off, 0, 0);
+        for (int i = 0; i < DW; i++) {
+            const uint32_t at = w_row[i] + (uint32_t)u * L::UB;
+            KH_LDS_LOAD(wsrc.r, st + L::OW + (i * WAVES + wave) * 1024, 16,
+                        on && w_row[i] != NONE ? (at & ~3u) + w_piece[i] : NONE);
         }
 #pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int ci = threadIdx.x + i * T, j = ci % NX, r = ci / NX;
-            const bool on = ci < RM * NX && m0 + r < a.rows && u * NX + j < a.k / G;
-            const uint32_t off = on ? (uint32_t)(((m0 + r) * (a.k / G) + u * NX + j) * 4) : NONE;
-            st.x[i] = __builtin_amdgcn_raw_buffer_load_b32(xsrc.r, (int)off, 0, 0);
+        for (int i = 0; i < DS; i++) {
+            const bool in = on && s_base[i] != NONE && u * NS + (int)s_j[i] < a.k / 32;
+            KH_LDS_LOAD(ssrc.r, st + L::OS + (i * WAVES + wave) * 256, 4, in ? s_base[i] + u * NS * 4 : NONE);
         }
-    };
-    auto stage_store = [&](const Stage &st, int buf) __attribute__((always_inline)) {
-        uint8_t *base = lds + buf * SB;
 #pragma unroll
-        for (int i = 0; i < CPT; i++) {
-            const int ci = threadIdx.x + i * T;
-            const int o = ci % (U / 16), rp = ci / (U / 16);
-            if (ci >= CC) continue;
-            uint8_t *to = base + rp * RS + 16 * o;
-            if (RS % 16 == 0) {
-                *reinterpret_cast<lanes::u32x4 *>(to) = st.c[i];
-            } else {  // rows 8-byte aligned
-                reinterpret_cast<lanes::u32x2 *>(to)[0] = lanes::u32x2{st.c[i].x, st.c[i].y};
-                reinterpret_cast<lanes::u32x2 *>(to)[1] = lanes::u32x2{st.c[i].z, st.c[i].w};
-            }
-        }
-        float *sx = reinterpret_cast<float *>(base + P * RM * RS);
-#pragma unroll
-        for (int i = 0; i < SPT; i++) {
-            const int ci = threadIdx.x + i * T, j = ci % NS, r = ci / NS;
-            if (ci < RM * NS) sx[j * RM + r] = __uint_as_float(st.s[i]);
-        }
-        float *xs = sx + NS * RM;
-#pragma unroll
-        for (int i = 0; i < XPT; i++) {
-            const int ci = threadIdx.x + i * T, j = ci % NX, r = ci / NX;
-            if (ci < RM * NX) xs[j * RM + r] = __uint_as_float(st.x[i]);
+        for (int i = 0; i < DX; i++) {
+            const bool in = on && x_base[i] != NONE && u * NX + (int)x_j[i] < a.k / G;
+            KH_LDS_LOAD(xsrc.r, st + L::OX + (i * WAVES + wave) * 256, 4, in ? x_base[i] + u * NX * 4 : NONE);
         }
     };
 
@@ -568,18 +623,19 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
         for (int t = 0; t < WN; t++) acc[i][t] = v16f{};
 
     using Regs = typename F::Regs;
-    auto compute = [&](const Regs (&R)[WN], int u, int buf) __attribute__((always_inline)) {
-        const uint8_t *base = lds + buf * SB;
-        const float *sx = reinterpret_cast<const float *>(base + P * RM * RS);
-        const float *xs = sx + NS * RM;
+    // Unit u from stage `slot`; `then` (the next unit's loads) runs once this
+    // unit's first LDS reads are issued.
+    auto compute = [&](int u, int slot, auto then) __attribute__((always_inline)) {
+        const uint8_t *st = lds + slot * L::SB;
+        const float *sx = reinterpret_cast<const float *>(st + L::OS);
+        const float *xs = reinterpret_cast<const float *>(st + L::OX);
+        Regs R[WN];
         float sc[WN][NG], mn[WN][NG];
 #pragma unroll
         for (int t = 0; t < WN; t++) {
-            F::scales(R[t], sc[t], mn[t]);
-            if (U == 128)
-#pragma unroll
-                for (int j = 0; j < NG; j++)
-                    if (u * U + j * G >= a.k) sc[t][j] = 0.0f, mn[t][j] = 0.0f;
+            const int col = wc + t * 32 + c;
+            const uint32_t shift = L::ODD ? (((uint32_t)(g0 + col) * row_bytes + (uint32_t)u * L::UB) & 3u) : 0u;
+            F::load(R[t], Lds{st + L::OW}, (uint32_t)(col * CW * 16) + shift, 0, h);
         }
         // The steps (group j, weight tile t, row tile i) in order, as a
         // pipeline: the MFMAs of a step are issued before the VALU work of
@@ -588,37 +644,58 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
         // step ahead of all VALU work, whose results would not fit in the
         // registers.
         constexpr int NQ = NG * WN * WM;
-        CodeT av[WM][P], bw;
-        float xa[WM], sw;
+        CodeT av[WM][P], an[WM][P], bw;
+        float xa[WM], xn[WM], sw;
         v16i dp[P];
         v16f sp;
+        // The A operands and activation scales of group j, read a group
+        // ahead of their use.
         auto a_operands = [&](int j) __attribute__((always_inline)) {
 #pragma unroll
             for (int i = 0; i < WM; i++) {
+                const int r = wr + i * 32 + c;
+                // Group j, half h: chunk 2j + h (groups of 32) or bytes 8h of
+                // chunk j (groups of 16).
+                const int o = G == 32 ? 2 * j + h : j, within = G == 32 ? 0 : 8 * h;
 #pragma unroll
                 for (int p = 0; p < P; p++)
-                    av[i][p] = *reinterpret_cast<const CodeT *>(base + (p * RM + i * 32 + c) * RS + j * G +
-                                                                (G / 2) * h);
-                xa[i] = h ? 0.0f : sx[(j * G / 32) * RM + i * 32 + c];
+                    an[i][p] = *reinterpret_cast<const CodeT *>(
+                        st + L::OA + (p * RM + r) * AW * 16 + (o ^ L::swz(r)) * 16 + within);
+                xn[i] = h ? 0.0f : sx[r * NS + j * G / 32];
             }
         };
-        // The unit's sums start from its first group's products; they join
-        // the running sums at the end of the unit (a sum in two levels).
-        v16f part[WM][WN];
-        auto finish = [&](int i, int t, bool first) __attribute__((always_inline)) {
+        a_operands(0);
+        then();
+#pragma unroll
+        for (int t = 0; t < WN; t++) {
+            F::scales(R[t], sc[t], mn[t]);
+            if (U == 128)
+#pragma unroll
+                for (int j = 0; j < NG; j++)
+                    if (u * U + j * G >= a.k) sc[t][j] = 0.0f, mn[t][j] = 0.0f;
+        }
+        auto finish = [&](int i, int t) __attribute__((always_inline)) {
 #pragma unroll
             for (int v = 0; v < 16; v++) {
                 float dot;
                 if (P == 3) dot = fmaf((float)dp[0][v], a.hi, (float)((dp[1][v] << a.shift) + dp[2][v]));
                 else dot = (float)dp[0][v];
-                part[i][t][v] = first ? dot * sp[v] : fmaf(dot, sp[v], part[i][t][v]);
+                acc[i][t][v] = fmaf(dot, sp[v], acc[i][t][v]);
             }
-            KH_PIN(part[i][t]);
+            KH_PIN(acc[i][t]);
         };
 #pragma unroll
         for (int q = 0; q < NQ; q++) {
             const int j = q / (WN * WM), t = (q / WM) % WN, i = q % WM;
-            if (t == 0 && i == 0) a_operands(j);
+            if (t == 0 && i == 0) {
+#pragma unroll
+                for (int ii = 0; ii < WM; ii++) {
+#pragma unroll
+                    for (int p = 0; p < P; p++) av[ii][p] = an[ii][p];
+                    xa[ii] = xn[ii];
+                }
+                if (j + 1 < NG) a_operands(j + 1);
+            }
             if (i == 0) {
                 bw = F::codes(R[t], j, h);
                 sw = h ? 0.0f : sc[t][j];
@@ -633,7 +710,7 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
             KH_PIN(xa[i]);
             KH_PIN(sw);
             const v16f sq = __builtin_amdgcn_mfma_f32_32x32x2f32(xa[i], sw, v16f{}, 0, 0, 0);
-            if (q > 0) finish((q - 1) % WM, ((q - 1) / WM) % WN, q - 1 < WN * WM);
+            if (q > 0) finish((q - 1) % WM, ((q - 1) / WM) % WN);
 #pragma unroll
             for (int p = 0; p < P; p++) dp[p] = dq[p];
             sp = sq;
@@ -642,7 +719,7 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
                     // Groups j - 1 (k-slot 0) and j (k-slot 1).
 #pragma unroll
                     for (int ii = 0; ii < WM; ii++) {
-                        float xm = xs[(j - 1 + h) * RM + ii * 32 + c];
+                        float xm = xs[(wr + ii * 32 + c) * NX + j - 1 + h];
                         KH_PIN(xm);
 #pragma unroll
                         for (int tt = 0; tt < WN; tt++) {
@@ -655,50 +732,40 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
                 }
             }
         }
-        finish(WM - 1, WN - 1, NQ == WN * WM);
-        // The unit's minimum term joins with it: two separate sums over all
-        // of K would cancel in the end.
+        finish(WM - 1, WN - 1);
+        if constexpr (F::MIN) {
+            // The unit's minimum term joins the sums unit by unit: two
+            // separate sums over all of K would cancel in the end.
 #pragma unroll
-        for (int i = 0; i < WM; i++)
+            for (int i = 0; i < WM; i++)
 #pragma unroll
-            for (int t = 0; t < WN; t++) {
+                for (int t = 0; t < WN; t++) {
 #pragma unroll
-                for (int v = 0; v < 16; v++) {
-                    float y = part[i][t][v];
-                    if constexpr (F::MIN) y = y + low[i][t][v];
-                    acc[i][t][v] = acc[i][t][v] + y;
+                    for (int v = 0; v < 16; v++) acc[i][t][v] = acc[i][t][v] + low[i][t][v];
+                    KH_PIN(acc[i][t]);
                 }
-                KH_PIN(acc[i][t]);
-            }
+        }
     };
 
-    // The K loop: stage u + 1 and the weights of u + 1 load while u is
-    // multiplied.
-    Regs R0[WN], R1[WN];
-    Stage st;
-    auto wload = [&](Regs (&R)[WN], int u) __attribute__((always_inline)) {
-        const bool on = u < u1;
+    // The K loop over a ring of S stages: unit u waits for its own loads
+    // (the D (S - 2) loads of the later units may still run), meets the
+    // other waves at a barrier (their loads of u are in; their reads of u - 1
+    // are done), loads unit u + S - 1 into the stage u - 1 used, multiplies.
+    // A bare s_barrier: a fenced one would wait for every load in flight.
 #pragma unroll
-        for (int t = 0; t < WN; t++) F::load(R[t], src, on ? ro[t] : NONE, on ? u : 0, h);
-    };
-    if (u0 < u1) {
-        stage_load(st, u0);
-        wload(R0, u0);
-        stage_store(st, 0);
-        __syncthreads();
+    for (int s = 0; s + 1 < S; s++) issue(u0 + s, s);
+    for (int u = u0; u < u1; u += S) {
+#pragma unroll
+        for (int s = 0; s < S; s++) {
+            if (u + s < u1) {
+                wait_vm<L::D * (S - 2)>();
+                __builtin_amdgcn_s_barrier();
+                compute(u + s, s, [&]() __attribute__((always_inline)) { issue(u + s + S - 1, (s + S - 1) % S); });
+            }
+        }
     }
-    auto step = [&](Regs (&Rc)[WN], Regs (&Rn)[WN], int u) __attribute__((always_inline)) {
-        const bool more = u + 1 < u1;
-        if (more) stage_load(st, u + 1);
-        wload(Rn, u + 1);
-        compute(Rc, u, (u - u0) & 1);
-        if (more) stage_store(st, (u + 1 - u0) & 1);
-        __syncthreads();
-    };
-    for (int u = u0; u < u1; u += 2) {
-        step(R0, R1, u);
-        if (u + 1 < u1) step(R1, R0, u + 1);
-    }
+    // No load may still write LDS when the workgroup ends.
+    wait_vm<0>();
 
     // Lane (c, h), register v of a tile holds row 8 (v / 4) + 4h + v % 4,
     // column c.
@@ -706,12 +773,12 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
     for (int i = 0; i < WM; i++)
 #pragma unroll
         for (int t = 0; t < WN; t++) {
-            const int64_t n = n0 + t * 32 + c;
-            if (n >= (int64_t)a.n[mat]) continue;
+            const int64_t n = g0 + wc + t * 32 + c;
+            if (n >= nmat) continue;
             const uint64_t col = a.col0[mat] + (uint64_t)n;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                const int m = m0 + wr + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
                 if (m >= a.rows) continue;
                 const float y = acc[i][t][v];
                 if (a.ks == 1) store_out(a.out_kind, a.out, (uint64_t)m * a.out_stride + col, y);
@@ -720,27 +787,66 @@ __global__ __launch_bounds__(64 * WAVES) void mm_kernel(MmArgs a) {
         }
 }
 
-// Rows of activations a workgroup takes: 64 with bytes, 32 with three
-// planes (LDS).
-template <class F, int P>
-hipError_t launch_fp(const MmArgs &a, hipStream_t s) {
+// The kernels of a format: bytes take two groups of waves of 64 rows each
+// above 64 rows, two of 32 rows above 32 rows, one of 32 rows below; three
+// planes take one group of 32 rows (LDS).
+template <class F, int P, int WM, int WMG>
+hipError_t launch_w(const MmArgs &a, hipStream_t s) {
+    using L = Plan<F, P, WM, WMG, wn_of<F, P, WM, WMG>()>;
+    static_assert(L::FITS, "two stages fit in LDS");
+    constexpr size_t bytes = (size_t)L::STAGES * L::SB;
+    static bool ready = false;
+    if (!ready) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mm_kernel<F, P, WM, WMG>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+        if (e != hipSuccess) return e;
+        ready = true;
+    }
     const int groups = a.ngroups * a.ks;
-    dim3 grid((unsigned)((groups + XCDS - 1) / XCDS * XCDS * a.mtiles)), block(64 * WAVES);
-    constexpr size_t lds1 = 2 * stage_bytes<F, P, 32>(), lds2 = 2 * stage_bytes<F, P, 64>();
-    if constexpr (P == 1)
-        if (a.wm == 2) {
-            hipLaunchKernelGGL((mm_kernel<F, P, 2>), grid, block, lds2, s, a);
-            return hipGetLastError();
-        }
-    if (a.wm == 1)
-        hipLaunchKernelGGL((mm_kernel<F, P, 1>), grid, block, lds1, s, a);
-    else
-        return hipErrorInvalidValue;
+    dim3 grid((unsigned)((groups + XCDS - 1) / XCDS * XCDS * a.mtiles)), block(64 * L::WAVES);
+    hipLaunchKernelGGL((mm_kernel<F, P, WM, WMG>), grid, block, bytes, s, a);
     return hipGetLastError();
 }
 
+// The shapes of the kernel a launch of `rows` rows takes: (wm, wmg).
+inline void shape_of(int planes, int rows, int &wm, int &wmg) {
+    if (planes == 1) {
+        wm = rows > 64 ? 2 : 1;
+        wmg = rows > 32 ? 2 : 1;
+    } else {
+        wm = 1;
+        wmg = 1;
+    }
+}
+
+template <class F, int P>
+hipError_t launch_fp(const MmArgs &a, hipStream_t s) {
+    if constexpr (P == 1) {
+        if (a.wm == 2 && a.wmg == 2) return launch_w<F, 1, 2, 2>(a, s);
+        if (a.wm == 1 && a.wmg == 2) return launch_w<F, 1, 1, 2>(a, s);
+        if (a.wm == 1 && a.wmg == 1) return launch_w<F, 1, 1, 1>(a, s);
+    } else {
+        if (a.wm == 1 && a.wmg == 1) return launch_w<F, 3, 1, 1>(a, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+// Weight rows of a column group (a workgroup's).
 template <class F>
-hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s) {
+int cols_f(int planes, int wm, int wmg) {
+    if (planes == 3) return Plan<F, 3, 1, 1, wn_of<F, 3, 1, 1>()>::NCOLS;
+    if (wm == 2) return Plan<F, 1, 2, 2, wn_of<F, 1, 2, 2>()>::NCOLS;
+    if (wmg == 2) return Plan<F, 1, 1, 2, wn_of<F, 1, 1, 2>()>::NCOLS;
+    return Plan<F, 1, 1, 1, wn_of<F, 1, 1, 1>()>::NCOLS;
+}
+
+// cols >= 0: the weight rows of a column group instead of a launch.
+template <class F>
+hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s, int *cols) {
+    if (cols) {
+        *cols = cols_f<F>(planes, a.wm, a.wmg);
+        return hipSuccess;
+    }
     if (planes == 1) return launch_fp<F, 1>(a, s);
     if (planes == 3) return launch_fp<F, 3>(a, s);
     return hipErrorInvalidValue;

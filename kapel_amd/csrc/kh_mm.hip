@@ -21,9 +21,9 @@ __global__ void mm_reduce_kernel(MmArgs a) {
 }  // namespace mm
 
 
-hipError_t mm_kquants(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s);
-hipError_t mm_blocks(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s);
-hipError_t mm_groups(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s);
+hipError_t mm_kquants(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s, int *cols);
+hipError_t mm_blocks(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s, int *cols);
+hipError_t mm_groups(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s, int *cols);
 
 int mm_group(uint32_t fmt, uint32_t group) {
     switch (fmt) {
@@ -36,16 +36,39 @@ int mm_group(uint32_t fmt, uint32_t group) {
     }
 }
 
-hipError_t launch_mm(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s) {
+namespace {
+hipError_t dispatch(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s, int *cols) {
     switch (fmt) {
     case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K:
-        return mm_kquants(fmt, planes, a, s);
+        return mm_kquants(fmt, planes, a, s, cols);
     case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1: case KH_Q8_0:
-        return mm_blocks(fmt, planes, a, s);
+        return mm_blocks(fmt, planes, a, s, cols);
     case KH_INT8: case KH_INT4:
-        return mm_groups(fmt, group, planes, a, s);
+        return mm_groups(fmt, group, planes, a, s, cols);
     }
     return hipErrorInvalidValue;
+}
+}  // namespace
+
+hipError_t launch_mm(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s) {
+    return dispatch(fmt, group, planes, a, s, nullptr);
+}
+
+void mm_shape(int planes, int rows, int &wm, int &wmg) { mm::shape_of(planes, rows, wm, wmg); }
+
+int mm_cols(uint32_t fmt, uint32_t group, int planes, int rows) {
+    MmArgs a{};
+    mm::shape_of(planes, rows, a.wm, a.wmg);
+    int cols = 0;
+    return dispatch(fmt, group, planes, a, nullptr, &cols) == hipSuccess ? cols : 0;
+}
+
+int mm_unit(uint32_t fmt, uint32_t group) {
+    switch (fmt) {
+    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: return 256;
+    case KH_INT8: case KH_INT4: return group == 256 ? 256 : 128;
+    default: return 128;
+    }
 }
 
 hipError_t launch_mm_reduce(const MmArgs &a, hipStream_t s) {

@@ -3,20 +3,20 @@
 
 namespace kh {
 
-hipError_t mm_groups(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s) {
+hipError_t mm_groups(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s, int *cols) {
     if (fmt == KH_INT8) {
         switch (group) {
-        case 32: return mm::launch_f<mm::Int8G<32>>(a, planes, s);
-        case 64: return mm::launch_f<mm::Int8G<64>>(a, planes, s);
-        case 128: return mm::launch_f<mm::Int8G<128>>(a, planes, s);
-        case 256: return mm::launch_f<mm::Int8G<256>>(a, planes, s);
+        case 32: return mm::launch_f<mm::Int8G<32>>(a, planes, s, cols);
+        case 64: return mm::launch_f<mm::Int8G<64>>(a, planes, s, cols);
+        case 128: return mm::launch_f<mm::Int8G<128>>(a, planes, s, cols);
+        case 256: return mm::launch_f<mm::Int8G<256>>(a, planes, s, cols);
         }
     } else if (fmt == KH_INT4) {
         switch (group) {
-        case 32: return mm::launch_f<mm::Int4G<32>>(a, planes, s);
-        case 64: return mm::launch_f<mm::Int4G<64>>(a, planes, s);
-        case 128: return mm::launch_f<mm::Int4G<128>>(a, planes, s);
-        case 256: return mm::launch_f<mm::Int4G<256>>(a, planes, s);
+        case 32: return mm::launch_f<mm::Int4G<32>>(a, planes, s, cols);
+        case 64: return mm::launch_f<mm::Int4G<64>>(a, planes, s, cols);
+        case 128: return mm::launch_f<mm::Int4G<128>>(a, planes, s, cols);
+        case 256: return mm::launch_f<mm::Int4G<256>>(a, planes, s, cols);
         }
     }
     return hipErrorInvalidValue;

@@ -46,6 +46,9 @@ struct uint2 {
 struct float4 {
     float x, y, z, w;
 };
+struct uint4 {
+    unsigned x, y, z, w;
+};
 
 namespace emu {
 
@@ -239,6 +242,16 @@ inline typename BufVec<N>::type buf_load(const BufferRsrc &r, int off) {
     return out;
 }
 
+// buffer_load_* ... lds: `size` bytes of each lane at offset off, to lds +
+// size * lane (dwords past num_records read as zero).
+inline void lds_load(const BufferRsrc &r, void *lds, int size, uint32_t off) {
+    uint8_t *dst = static_cast<uint8_t *>(lds) + size * lane_id();
+    for (int i = 0; i < size / 4; i++) {
+        uint32_t v = buf_dword(r, (int)(off + 4 * i));
+        std::memcpy(dst + 4 * i, &v, 4);
+    }
+}
+
 inline int frexp_exp(float v) {
     int e = 0;
     if (std::isfinite(v)) std::frexp(v, &e);
@@ -276,6 +289,9 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(...) emu::mfma32_f32x2(__VA_ARGS__)
 #define __builtin_amdgcn_sched_barrier(m) ((void)0)
 #define KH_PIN(x) ((void)0)
+#define KH_LDS_LOAD(rsrc, lds, size, voff) emu::lds_load((rsrc), (void *)(lds), (size), (uint32_t)(voff))
+#define __builtin_amdgcn_s_waitcnt(n) ((void)0)
+#define __builtin_amdgcn_s_barrier() (emu::block.all->arrive_and_wait())
 #define __builtin_amdgcn_perm(hi, lo, s) emu::perm((hi), (lo), (s))
 #define __builtin_amdgcn_alignbyte(hi, lo, s) emu::alignbyte((hi), (lo), (s))
 #define __builtin_amdgcn_mov_dpp(v, c, r, b, z) emu::mov_dpp((v), (c), (r), (b), (z))
@@ -297,6 +313,10 @@ typedef emu::BufferRsrc __amdgpu_buffer_rsrc_t;
     emu::launch(kernel, dim3(grid), dim3(threads), (size_t)(lds), __VA_ARGS__)
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
+enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
+inline hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int bytes) {
+    return bytes <= (int)emu::LDS_BYTES ? hipSuccess : hipErrorInvalidValue;
+}
 enum hipMemcpyKind { hipMemcpyDeviceToDevice = 3 };
 inline hipError_t hipMemcpyAsync(void *dst, const void *src, size_t n, hipMemcpyKind, hipStream_t) {
     std::memcpy(dst, src, n);
