@@ -160,6 +160,42 @@ MmSplit mm_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std:
     return m;
 }
 
+// The decode kernel with its weights staged in LDS (gemv2_kernel): for one
+// row of f32 activations or up to four of bytes, without block dots.  Tiles a
+// workgroup as the small-M split picks them (halved while LDS is short);
+// multiplying waves as many as fit (up to 16 with the preparing ones, not
+// more than the units); copies of 1 KiB a wave for its units of every tile.
+struct Gemv2 {
+    bool ok = false;
+    int tiles, npw, kw, tb;
+};
+
+Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, int tiles_total, int tiles) {
+    Gemv2 p;
+    const int unit = gemv_unit(fmt, group);
+    const int len = (int)kh_block_len(fmt, group), bytes = (int)kh_block_bytes(fmt, group);
+    if (!unit || !len) return p;
+    const int ub = (len >= unit ? 1 : unit / len) * bytes;
+    const int cw = (ub + (bytes % 4 ? 2 : 0) + 15) / 16;
+    const int units = (int)div_up(k, unit);
+    const int quads = rows * units * unit / 4;
+    p.npw = std::max(1, std::min(4, (int)div_up(quads, 512)));
+    for (int t = tiles; t >= 1; t /= 2)
+        for (int kw = std::min(16 - p.npw, units); kw >= 1; kw--) {
+            const int upw = (int)div_up(units, kw);
+            const int tb = (int)div_up(t * 16 * cw * upw, 64);
+            if (gemv2_lds(rows, planes, units, unit, t, kw, tb) <= 160 * 1024) {
+                p.ok = true;
+                p.tiles = t;
+                p.kw = kw;
+                p.tb = tb;
+                return p;
+            }
+        }
+    (void)tiles_total;
+    return p;
+}
+
 // The workspace: the counters of the segment split (fixed, first), the
 // prepared activations, then the partial sums.
 struct Layout {
@@ -212,6 +248,7 @@ struct Launch {
     bool gemv;        // the small-M product (all rows in one launch)
     bool mm;          // the many-row product (rows r0 .. r0 + rows)
     GemvSplit gsplit;
+    Gemv2 g2;         // the decode kernel staged in LDS, when it applies
     Split split;
     MmSplit msplit;
 };
@@ -250,6 +287,15 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
             L.r0 = 0;
             L.rows = (int)std::min<uint64_t>(rows, gemv_max_rows(planes));
             L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes, (int)div_up(rows, L.rows), L.rows < (int)rows);
+            L.g2 = Gemv2{};
+            if (L.rows == (int)rows && (planes == 3 ? rows == 1 : rows <= 4)) {
+                // A workgroup's tiles in one matrix: several only when every
+                // matrix is a whole number of them.
+                int most = L.gsplit.tiles;
+                for (uint32_t m : L.members)
+                    while (most > 1 && div_up(weights[m].n, 16) % most) most /= 2;
+                L.g2 = gemv2_plan(w.format, w.group, k, L.rows, planes, L.tiles, most);
+            }
             fn(L);
             continue;
         }
@@ -428,6 +474,13 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.out = out;
             a.out_stride = c.width;
             a.width = c.width;
+            if (L.g2.ok) {
+                a.dma = 1;
+                a.tiles = L.g2.tiles;
+                a.npw = L.g2.npw;
+                a.kw = L.g2.kw;
+                a.tb = L.g2.tb;
+            }
             err = launch_gemv(w.format, w.group, planes, a, s);
             return;
         }

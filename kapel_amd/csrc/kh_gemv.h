@@ -453,11 +453,268 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// The decode product with its weights staged in LDS by direct loads (few
+// activation rows, every matrix format the lane readers know).
+//
+// A workgroup takes `tiles` tiles of 16 weight rows over all of K.  Its first
+// `npw` waves prepare the activations in LDS (x_load / x_prepare); the other
+// `kw` waves split the units of K between them (wave c takes units c, c + kw,
+// ...).  Each of those waves first copies its own units of all its tiles
+// from HBM into LDS with buffer_load ... lds (16 bytes a lane, consecutive
+// lanes to consecutive LDS, so every copy is coalesced and holds no
+// register), tile after tile: all of a workgroup's weight bytes are in flight
+// at once.  It then meets the preparing waves at a barrier and multiplies
+// each tile as soon as its own copies have landed (its own vmcnt: no wave
+// waits for another's loads), reading the weights from LDS through the same
+// lane readers.  The sums of the waves are added in wave order by the
+// preparing waves, which write the outputs.
+//
+// LDS of a wave's weights: [tile][unit][row of 16][CW chunks] in TB copies
+// of 64 chunks; a row's unit is its block (or blocks) from the dword at or
+// below its start.
+
+// s_waitcnt vmcnt(n) for a wave-uniform n (clamped to 63: waiting for more
+// than needed is safe).
+__device__ __forceinline__ void wait_vm_n(int n) {
+#define KH_VM(N) case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | (7 << 4) | (15 << 8)); break;
+    switch (n < 63 ? n : 63) {
+        KH_VM(0) KH_VM(1) KH_VM(2) KH_VM(3) KH_VM(4) KH_VM(5) KH_VM(6) KH_VM(7) KH_VM(8) KH_VM(9)
+        KH_VM(10) KH_VM(11) KH_VM(12) KH_VM(13) KH_VM(14) KH_VM(15) KH_VM(16) KH_VM(17) KH_VM(18) KH_VM(19)
+        KH_VM(20) KH_VM(21) KH_VM(22) KH_VM(23) KH_VM(24) KH_VM(25) KH_VM(26) KH_VM(27) KH_VM(28) KH_VM(29)
+        KH_VM(30) KH_VM(31) KH_VM(32) KH_VM(33) KH_VM(34) KH_VM(35) KH_VM(36) KH_VM(37) KH_VM(38) KH_VM(39)
+        KH_VM(40) KH_VM(41) KH_VM(42) KH_VM(43) KH_VM(44) KH_VM(45) KH_VM(46) KH_VM(47) KH_VM(48) KH_VM(49)
+        KH_VM(50) KH_VM(51) KH_VM(52) KH_VM(53) KH_VM(54) KH_VM(55) KH_VM(56) KH_VM(57) KH_VM(58) KH_VM(59)
+        KH_VM(60) KH_VM(61) KH_VM(62)
+        default: KH_VM(63)
+    }
+#undef KH_VM
+}
+
+// LDS waits and a bare barrier (a fenced __syncthreads would also wait for
+// every load in flight).
+__device__ __forceinline__ void lds_barrier() {
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4) | (0 << 8));  // lgkmcnt(0)
+    __builtin_amdgcn_s_barrier();
+}
+
+#ifndef KH_LDS_LOAD
+#define KH_LDS_LOAD(rsrc, lds, size, voff) \
+    __builtin_amdgcn_raw_ptr_buffer_load_lds((rsrc), (__attribute__((address_space(3))) void *)(lds), (size), (int)(voff), 0, 0, 0)
+#endif
+
+// Bytes of a unit's copy: its block (several blocks of 32-element formats,
+// one block, shared by two units, for Kapel groups of 256), and 16-byte
+// chunks of it from the dword below its start.
+template <class F>
+struct Unit {
+    static constexpr int PER = F::BLEN >= F::U ? 1 : F::U / F::BLEN;  // blocks a copy
+    static constexpr int UB = PER * F::BYTES;
+    static constexpr bool ODD = F::BYTES % 4 != 0;
+    static constexpr int CW = (UB + (ODD ? 2 : 0) + 15) / 16;
+    // The first block of unit u, and u within that block's units.
+    __device__ static uint32_t block(int u) { return (uint32_t)((int64_t)u * F::U / F::BLEN); }
+    __device__ static int local(int u) { return F::BLEN > F::U ? u % (F::BLEN / F::U) : 0; }
+};
+
+template <class F, int P, int MT, int XK>
+__global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
+    using UN = Unit<F>;
+    constexpr int U = F::U, CW = UN::CW;
+    constexpr int ACC = P == 3 ? MT : 4 * MT;
+    constexpr int NG = F::GS == 16 ? F::STEPS : F::STEPS / 2;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    const int group = blockIdx.x;
+    const int t0 = group * a.tiles;
+    if (t0 >= a.total_tiles) return;
+    const int T = min(a.tiles, a.total_tiles - t0);
+    const int rows = a.rows;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n16 = lane & 15;
+    const int span = a.units * U;
+    const int TB = a.tb;
+
+    // LDS: planes [rows][P][span], zeros [span], info [rows][span / 32],
+    // sums [kw][tiles][16][rows], weights [kw][TB KiB].
+    int8_t *planes = reinterpret_cast<int8_t *>(lds + 16);
+    int8_t *zeros = planes + (size_t)rows * P * span;
+    float4 *info = reinterpret_cast<float4 *>(zeros + span);
+    float *sums = reinterpret_cast<float *>(info + (size_t)rows * (span / 32));
+    uint8_t *wl = reinterpret_cast<uint8_t *>(
+        ((uintptr_t)(sums + (size_t)a.kw * a.tiles * 16 * rows) + 15) & ~(uintptr_t)15);
+
+    // The matrix and row of a tile's row.
+    auto row_of = [&](int tile, int r, int &mat) {
+        mat = 0;
+        for (int i = 1; i < a.count; i++)
+            if (tile >= a.tile0[i]) mat = i;
+        return (int64_t)(tile - a.tile0[mat]) * 16 + r;
+    };
+
+    if (wave < a.npw) {
+        // ---- the activations, then (after the multiplying waves) the sums
+        for (int i = threadIdx.x; i < span / 16; i += 64 * a.npw)
+            reinterpret_cast<v4i *>(zeros)[i] = v4i{0, 0, 0, 0};
+        const XIn xin{a.x, rows, a.k, a.x_kind};
+        const int qpc = rows * span / 4;
+        for (int q0 = 0; q0 < qpc; q0 += 64 * a.npw * PASSES) {
+            float xv[PASSES][4];
+            x_load<XK>(xin, 0, span, q0, threadIdx.x, 64 * a.npw, xv);
+            x_prepare<P, XK>(xin, span, q0, threadIdx.x, 64 * a.npw, xv, planes, info);
+        }
+        lds_barrier();  // the activations are ready
+        lds_barrier();  // the sums are written
+        for (int o = threadIdx.x; o < T * 16 * rows; o += 64 * a.npw) {
+            const int t = o / (16 * rows), r = (o / rows) % 16, m = o % rows;
+            int mat;
+            const int64_t n = row_of(t0 + t, r, mat);
+            if (n >= (int64_t)a.n[mat]) continue;
+            float v = sums[((0 * a.tiles + t) * 16 + r) * rows + m];
+            for (int c = 1; c < a.kw; c++) v = v + sums[((c * a.tiles + t) * 16 + r) * rows + m];
+            store_out(a.out_kind, a.out, (uint64_t)m * a.out_stride + a.col0[mat] + (uint64_t)n, v);
+        }
+        return;
+    }
+
+    // ---- a multiplying wave: copy its units of every tile, then multiply
+    const int cw = wave - a.npw;
+    const int upw = (a.units - cw + a.kw - 1) / a.kw;  // its units
+    const int upm = (a.units + a.kw - 1) / a.kw;       // units of the wave with most
+    const int tchunks = 16 * upm * CW;                  // chunks of one tile's block
+    uint8_t *mine = wl + (size_t)cw * TB * 1024;
+    // TB copies of 64 chunks over [tile][unit][row][CW], in order.  The
+    // tiles of a workgroup lie in one matrix (the host takes several only
+    // when every matrix is a whole number of them).
+    int wmat;
+    const int64_t row0 = row_of(t0, 0, wmat);
+    const lanes::Src src = lanes::source(a.w[wmat], a.wbytes[wmat]);
+    const int64_t nmat = (int64_t)a.n[wmat];
+    for (int i = 0; i < TB; i++) {
+        // A copy spans at most two tiles (a tile's block is over 64 chunks).
+        const int ti = __builtin_amdgcn_readfirstlane(i * 64 / tchunks);
+        const int ci = i * 64 + lane, t = ci >= (ti + 1) * tchunks ? ti + 1 : ti, rem = ci - t * tchunks;
+        const int j = rem / (16 * CW), r = (rem / CW) % 16, c = rem % CW;
+        const int64_t n = row0 + t * 16 + r;
+        const int u = cw + j * a.kw;
+        const bool on = t < T && j < upw && n < nmat;
+        const uint32_t at = (uint32_t)n * (uint32_t)a.row_bytes + UN::block(u) * F::BYTES;
+        KH_LDS_LOAD(src.r, mine + i * 1024, 16, on ? (at & ~3u) + 16u * c : lanes::NONE);
+    }
+    lds_barrier();  // the activations are ready
+
+    // The A operand of this lane: row i = lane % 16 of each MFMA is (plane
+    // or activation row) j = i % 4 of lane group i / 4, in that lane group's
+    // k-slice only; elsewhere it reads zeros.
+    const int ai = lane & 15, aj = ai & 3;
+    const bool a_lane = (ai >> 2) == (lane >> 4);
+    int a_off[MT];
+#pragma unroll
+    for (int mi = 0; mi < MT; mi++) {
+        int m = P == 3 ? mi : 4 * mi + aj, p = P == 3 ? aj : 0;
+        bool on = a_lane && p < P && m < rows;
+        a_off[mi] = (on ? (m * P + p) * span : (int)(zeros - planes)) + F::xpos(g, 0);
+    }
+    const float4 *my_info = info + F::xpos(g, 0) / 32;
+    const int blocks32 = a.k / 32;
+
+    for (int t = 0; t < T; t++) {
+        int mat;
+        const int64_t n = row_of(t0 + t, n16, mat);
+        // This tile's copies are the first ceil((t + 1) tchunks / 64).
+        wait_vm_n(TB - (((t + 1) * tchunks + 63) >> 6));
+        float acc[ACC];
+#pragma unroll
+        for (int i = 0; i < ACC; i++) acc[i] = 0.0f;
+        for (int jj = 0; jj < upw; jj++) {
+            const int u = cw + jj * a.kw;
+            const bool ok = U == 256 || 4 * u + g < blocks32;
+            const uint32_t at = (uint32_t)n * (uint32_t)a.row_bytes + UN::block(u) * F::BYTES;
+            typename F::Regs R;
+            F::load(R, lanes::LdsSrc{mine}, (uint32_t)((t * tchunks + (jj * 16 + n16) * CW) * 16) + (at & 3u),
+                    UN::local(u), g);
+            float sc[NG], mn[NG];
+            F::scales(R, g, sc, mn);
+            v4i c[MT];
+#pragma unroll
+            for (int s = 0; s < F::STEPS; s++) {
+                v4i bw = F::codes(R, s, g);
+                if (U == 128 && !ok) bw = v4i{0, 0, 0, 0};
+                if (F::GS == 16 || (s & 1) == 0)
+#pragma unroll
+                    for (int mi = 0; mi < MT; mi++) c[mi] = v4i{0, 0, 0, 0};
+                const int xo = u * U + F::xpos(g, s) - F::xpos(g, 0);
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+                    v4i av = *reinterpret_cast<const v4i *>(planes + a_off[mi] + xo);
+                    c[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bw, c[mi], 0, 0, 0);
+                }
+                if (!ok || !(F::GS == 16 || (s & 1) == 1)) continue;
+                // The group of this step is complete: scale it.
+                const int s0 = F::GS == 16 ? s : s - 1, gi = F::GS == 16 ? s : s / 2;
+                const int blk = (u * U + F::xpos(g, s0) - F::xpos(g, 0)) / 32;
+                const bool second = ((F::xpos(g, s0) / 16) & 1) != 0;
+#pragma unroll
+                for (int mi = 0; mi < MT; mi++) {
+#pragma unroll
+                    for (int j = 0; j < (P == 3 ? 1 : 4); j++) {
+                        int m = P == 3 ? mi : 4 * mi + j;
+                        if (m >= rows) continue;
+                        float4 in = my_info[(size_t)m * (span / 32) + blk];
+                        float dot;
+                        if (P == 3) dot = fmaf((float)c[mi].x, a.hi, (float)((c[mi].y << a.shift) + c[mi].z));
+                        else dot = (float)c[mi][j];
+                        float xsum = F::GS == 32 ? in.y : (second ? in.w : in.z);
+                        float tt = fmaf(dot, sc[gi] * in.x, acc[m]);
+                        acc[m] = fmaf(-mn[gi], xsum, tt);
+                    }
+                }
+            }
+        }
+        // The four lane groups of each row in a fixed tree, then to LDS.
+#pragma unroll
+        for (int i = 0; i < ACC; i++) {
+            float v = acc[i];
+            v = v + __shfl_xor(v, 16);
+            acc[i] = v + __shfl_xor(v, 32);
+        }
+        if (g == 0)
+#pragma unroll
+            for (int i = 0; i < ACC; i++)
+                if (i < rows) sums[((cw * a.tiles + t) * 16 + n16) * rows + i] = acc[i];
+    }
+    wait_vm_n(0);
+    lds_barrier();  // the sums are written
+}
+
 namespace {
+
+template <class F, int P, int MT, int XK>
+hipError_t launch2(const GemvArgs &a, hipStream_t s, size_t lds) {
+    static bool ready = false;
+    if (!ready) {
+        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv2_kernel<F, P, MT, XK>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+        if (e != hipSuccess) return e;
+        ready = true;
+    }
+    const int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
+    hipLaunchKernelGGL((gemv2_kernel<F, P, MT, XK>), dim3((unsigned)groups), dim3(64 * (a.npw + a.kw)), lds, s, a);
+    return hipGetLastError();
+}
 
 template <class F, int P, int XK>
 hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
     int mt = P == 3 ? a.rows : (a.rows + 3) / 4;
+    if (a.dma) {
+        if (a.tb * 64 < a.tiles * 16 * Unit<F>::CW * ((a.units + a.kw - 1) / a.kw) || a.npw + a.kw > 16)
+            return hipErrorInvalidValue;
+        size_t lds = gemv2_lds(a.rows, P, a.units, F::U, a.tiles, a.kw, a.tb);
+        if (lds > 160 * 1024) return hipErrorInvalidValue;
+        if (mt <= 1) return launch2<F, P, 1, XK>(a, s, lds);
+        return hipErrorInvalidValue;
+    }
     int waves = a.tiles * a.kw;
     size_t lds = gemv_lds(a.rows, P, a.chunk, F::U, waves);
     const int groups = (a.total_tiles + a.tiles - 1) / a.tiles;

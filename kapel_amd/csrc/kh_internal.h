@@ -104,6 +104,9 @@ struct GemvArgs {
     // The planes' digits: v = a hi + (b << shift) + c (2^16, 8).
     float hi;
     int shift;
+    // The kernel with its weights staged in LDS (gemv2_kernel): `npw`
+    // preparing waves, `kw` multiplying waves, `tb` copies of 1 KiB a wave.
+    int dma, npw, tb;
 };
 
 // The many-row product (kh_mm.h): weights of one format in column groups of
@@ -166,6 +169,8 @@ int gemv_max_waves(int planes, int rows);
 // Bytes of LDS of one of its workgroups.
 size_t gemv_lds(int rows, int planes, int chunk, int unit, int waves);
 hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s);
+// LDS bytes of a workgroup of the decode kernel staged in LDS.
+size_t gemv2_lds(int rows, int planes, int units, int unit, int tiles, int kw, int tb);
 // The many-row product: the size of a format's scale groups (32 or 16; 0:
 // not read by it).
 int mm_group(uint32_t fmt, uint32_t group);

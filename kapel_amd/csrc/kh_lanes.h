@@ -85,6 +85,33 @@ __device__ __forceinline__ void run(uint32_t (&w)[(R + 3) / 4], const Src &src, 
     for (int i = 0; i < W; i++) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], s);
 }
 
+// The same reads from LDS (a workgroup's copy of the bytes): N dwords at a
+// multiple of 4, runs at even offsets.
+struct LdsSrc {
+    const uint8_t *p;
+};
+
+template <int N>
+__device__ __forceinline__ void ldb(uint32_t (&v)[N], const LdsSrc &s, uint32_t off) {
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(s.p + off);
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = w[i];
+}
+
+template <int R>
+__device__ __forceinline__ void run(uint32_t (&w)[(R + 3) / 4], const LdsSrc &src, uint32_t off) {
+    static_assert(R % 2 == 0, "even runs only");
+    constexpr int D = (R + 5) / 4, W = (R + 3) / 4;
+    const uint32_t s = off & 2u;
+    const uint32_t *p = reinterpret_cast<const uint32_t *>(src.p + (off - s));
+    uint32_t v[D + 1];
+#pragma unroll
+    for (int i = 0; i < D; i++) v[i] = p[i];
+    v[D] = 0u;
+#pragma unroll
+    for (int i = 0; i < W; i++) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], s);
+}
+
 __device__ __forceinline__ float f16(uint32_t h) { return __half2float(__ushort_as_half((uint16_t)h)); }
 __device__ __forceinline__ uint32_t byte_of(uint32_t w, int i) { return (w >> (8 * i)) & 0xffu; }
 // Dword i of a 16-byte vector held as four dwords.
@@ -125,11 +152,12 @@ __device__ __forceinline__ void k_pair(const uint32_t (&h)[4], int g, float (&s)
 }
 
 struct Q4K {
-    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 144;
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 144, BLEN = 256;
     struct Regs {
         uint32_t h[4], q[8];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + u * BYTES;
         ldb<4>(r.h, src, b);
         ldb<8>(r.q, src, b + 16 + 32 * g);
@@ -148,11 +176,12 @@ struct Q4K {
 // 176 bytes: as Q4_K with 32 bytes of fifth bits at 16: bit j of byte l is
 // the fifth bit of element 32j + l; nibbles at 48.
 struct Q5K {
-    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 176;
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 176, BLEN = 256;
     struct Regs {
         uint32_t h[4], qh[8], q[8];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + u * BYTES;
         ldb<4>(r.h, src, b);
         ldb<8>(r.qh, src, b + 16);
@@ -178,11 +207,12 @@ struct Q5K {
 // (128h + 32t + l) / 16.  Lane group g: h = g / 2, t % 2 = g % 2; step s:
 // t = g % 2 + 2(s / 2), l = 16(s % 2) .. + 15.  Codes are stored + 32.
 struct Q6K {
-    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 210;
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 210, BLEN = 256;
     struct Regs {
         uint32_t ql[8], qh[8], sc[2], d;
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + u * BYTES;
         int h = g >> 1, q = g & 1;
         run<32>(r.ql, src, b + 64 * h + 32 * q);
@@ -220,11 +250,12 @@ struct Q6K {
 // 2t of byte 16 + 32h + l; group e / 16.  Lane group g: h = g / 2, l =
 // 16(g % 2) .. + 15; step s: t = s.
 struct Q2K {
-    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 84;
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 84, BLEN = 256;
     struct Regs {
         uint32_t q[4], sc[2], dd;
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + u * BYTES;
         int h = g >> 1;
         ldb<4>(r.q, src, b + 16 + 32 * h + 16 * (g & 1));
@@ -256,11 +287,12 @@ struct Q2K {
 // of byte 32 + 32h + l, high bit 4h + t of byte l; value d scale ((low |
 // high << 2) - 4).  Lanes as Q2_K.
 struct Q3K {
-    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 110;
+    static constexpr int U = 256, STEPS = 4, GS = 16, BYTES = 110, BLEN = 256;
     struct Regs {
         uint32_t hm[4], q[4], sc[3], d;
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + u * BYTES;
         int h = g >> 1;
         run<16>(r.hm, src, b + 16 * (g & 1));
@@ -300,11 +332,12 @@ __device__ __forceinline__ void nib_codes(v4i &c, const uint32_t *q, int s) {
 
 // Q4_0: 18 bytes, d then 16 bytes (byte j: element j low, j + 16 high).
 struct Q4_0 {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 18;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 18, BLEN = 32;
     struct Regs {
         uint32_t w[5];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         run<18>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
@@ -323,11 +356,12 @@ struct Q4_0 {
 
 // Q4_1: 20 bytes, d, m, then nibbles; w = d q + m.
 struct Q4_1 {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 20;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 20, BLEN = 32;
     struct Regs {
         uint32_t w[5];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         ldb<5>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
@@ -352,11 +386,12 @@ __device__ __forceinline__ uint32_t spread4(uint32_t high, int j) {
 // w = d (q - 16).  Q5_1: 24 bytes, d, m, fifth bits, nibbles; w = d q + m.
 template <bool ONE>
 struct Q5x {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = ONE ? 24 : 22;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = ONE ? 24 : 22, BLEN = 32;
     struct Regs {
         uint32_t w[(BYTES + 3) / 4];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         const uint32_t b = row + (4 * u + g) * BYTES;
         if (ONE) ldb<6>(*reinterpret_cast<uint32_t(*)[6]>(r.w), src, b);
         else run<22>(*reinterpret_cast<uint32_t(*)[6]>(r.w), src, b);
@@ -386,11 +421,12 @@ using Q5_1 = Q5x<true>;
 
 // Q8_0: 34 bytes, d then 32 signed bytes (dtype.rs:375-378).
 struct Q8_0 {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 34;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 34, BLEN = 32;
     struct Regs {
         uint32_t w[9];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         run<34>(r.w, src, row + (4 * u + g) * BYTES);
     }
     __device__ static v4i codes(const Regs &r, int s, int) {
@@ -411,11 +447,12 @@ struct Q8_0 {
 // (dtype.rs:364-374).  Lane group g takes the 32 elements of piece 4u + g.
 template <int G>
 struct Int8G {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G, BLEN = G;
     struct Regs {
         uint32_t scale, q[8];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         int p = 4 * u + g;
         const uint32_t b = row + (32 * p / G) * BYTES;
         uint32_t sc[1];
@@ -435,11 +472,12 @@ struct Int8G {
 
 template <int G>
 struct Int4G {
-    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G / 2;
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 4 + G / 2, BLEN = G;
     struct Regs {
         uint32_t scale, q[4];
     };
-    __device__ static void load(Regs &r, const Src &src, uint32_t row, int u, int g) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
         int p = 4 * u + g;
         const uint32_t b = row + (32 * p / G) * BYTES;
         uint32_t sc[1];
