@@ -71,6 +71,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
+    ap.add_argument("--configs", default="1,3,4,5",
+                    help="which of the other configs to run (comma-separated), after config 2")
     ap.add_argument("--profile", choices=["gateup", "copy"],
                     help="only launch the [gate; up] call (or a 256 MiB device copy) "
                          "20 times, for rocprofv3 counter runs")
@@ -208,8 +210,8 @@ def main():
     tpath = os.path.join(ROOT, "profiles", "traffic.json")
     if os.path.exists(tpath):
         traffic = json.load(open(tpath)).get("gemv_q4k_gateup_m1_bytes_per_launch")
-    roofline = {"kernel": "gemv_kernel<Q4K, planes 3, 1 MFMA/step, 16 waves, f32 x> "
-                          "([gate; up], 16384 x 3072 Q4_K, M = 1)",
+    roofline = {"kernel": "gemv2_kernel<Q4K, 3 planes, 1 row, f32 x>: weights staged in LDS by direct "
+                          "loads ([gate; up], 16384 x 3072 Q4_K, M = 1)",
                 "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                 "algorithmic_bytes_per_launch": gate_bytes,
@@ -217,83 +219,88 @@ def main():
                 "timing": "HIP events around graph replays of 28 launches (rotated weights)"}
 
     configs = {}
-    if not args.no_configs:
-        # ---- config 3: the same layer, M = 64, byte activations ---------------
-        hip.with_byte_activations(True)
-        reserve(CALLS, layers[0], 64, True)
-        xs, outs = inputs_for(CALLS, host, 64)
-        s3, _ = timed([layer_step(l) for l in range(L)], 2 * L, L)
-        ops3 = 2 * 64 * sum(n * k for _, n, k, _ in LAYER)
-        configs["3"] = {"workload": "Llama-3.2-3B layer (Q4_K + Q6_K down), M = 64, byte activations",
-                        "ms_per_step": round(s3 * 1e3, 4), "tops": round(ops3 / s3 / 1e12, 2),
-                        "mfma_frac": round(ops3 / s3 / 1e12 / INT8_PEAK_TOPS, 4),
-                        "weight_gbps": round(layer_bytes / s3 / 1e9, 1)}
-        hip.with_byte_activations(False)
+    only = set() if args.no_configs else set(args.configs.split(","))
+    if only:
+        if "3" in only:
+            # ---- config 3: the same layer, M = 64, byte activations ---------------
+            hip.with_byte_activations(True)
+            reserve(CALLS, layers[0], 64, True)
+            xs, outs = inputs_for(CALLS, host, 64)
+            s3, _ = timed([layer_step(l) for l in range(L)], 2 * L, L)
+            ops3 = 2 * 64 * sum(n * k for _, n, k, _ in LAYER)
+            configs["3"] = {"workload": "Llama-3.2-3B layer (Q4_K + Q6_K down), M = 64, byte activations",
+                            "ms_per_step": round(s3 * 1e3, 4), "tops": round(ops3 / s3 / 1e12, 2),
+                            "mfma_frac": round(ops3 / s3 / 1e12 / INT8_PEAK_TOPS, 4),
+                            "weight_gbps": round(layer_bytes / s3 / 1e9, 1)}
+            hip.with_byte_activations(False)
 
-        # ---- config 1: Q4_0 8192 x 2048, M = 1 ---------------------------------
-        d1 = ka.quantize(ka.Q4_0, 0, synth.normal(0, 8192 * 2048, 0.02))  # seed 0, as config 1 says
-        copies = max(2, int(1.2e9 // d1.size))
-        w1 = [ka.QuantizedTensor(torch.from_numpy(d1).to(dev), ka.Q4_0, 0, 8192, 2048)
-              for _ in range(copies)]
-        x1 = torch.from_numpy(synth.normal(1, 2048, 1.0).reshape(1, 2048)).to(dev)
-        o1 = torch.empty((1, 8192), device=dev)
-        s1, _ = timed([(lambda w=w: hip.forward(op, [x1, w], out=o1)) for w in w1], 4 * copies, copies)
-        configs["1"] = {"workload": "Q4_0 8192 x 2048, M = 1, f32 activations",
-                        "us_per_call": round(s1 * 1e6, 2), "weight_gbps": round(d1.size / s1 / 1e9, 1)}
-        del w1
+        if "1" in only:
+            # ---- config 1: Q4_0 8192 x 2048, M = 1 ---------------------------------
+            d1 = ka.quantize(ka.Q4_0, 0, synth.normal(0, 8192 * 2048, 0.02))  # seed 0, as config 1 says
+            copies = max(2, int(1.2e9 // d1.size))
+            w1 = [ka.QuantizedTensor(torch.from_numpy(d1).to(dev), ka.Q4_0, 0, 8192, 2048)
+                  for _ in range(copies)]
+            x1 = torch.from_numpy(synth.normal(1, 2048, 1.0).reshape(1, 2048)).to(dev)
+            o1 = torch.empty((1, 8192), device=dev)
+            s1, _ = timed([(lambda w=w: hip.forward(op, [x1, w], out=o1)) for w in w1], 4 * copies, copies)
+            configs["1"] = {"workload": "Q4_0 8192 x 2048, M = 1, f32 activations",
+                            "us_per_call": round(s1 * 1e6, 2), "weight_gbps": round(d1.size / s1 / 1e9, 1)}
+            del w1
 
-        # ---- config 5: low-bit FFN, int4 attention, Q6_K output table, M in {1, 8}
-        c5 = {}
-        parts = [("up_q2k", ka.Q2K, 0, 12288, 4096), ("down_q2k", ka.Q2K, 0, 4096, 12288),
-                 ("up_q3k", ka.Q3K, 0, 12288, 4096), ("down_q3k", ka.Q3K, 0, 4096, 12288),
-                 ("up_q5k", ka.Q5K, 0, 12288, 4096), ("down_q5k", ka.Q5K, 0, 4096, 12288),
-                 ("q_int4", ka.INT4, 32, 4096, 4096)]
-        for name, fmt, group, n, k in parts:
-            d = ka.quantize(fmt, group, values(500 + len(c5), n * k))
-            copies = max(2, int(1.2e9 // d.size))
-            ws5 = [ka.QuantizedTensor(torch.from_numpy(d).to(dev), fmt, group, n, k) for _ in range(copies)]
+        if "5" in only:
+            # ---- config 5: low-bit FFN, int4 attention, Q6_K output table, M in {1, 8}
+            c5 = {}
+            parts = [("up_q2k", ka.Q2K, 0, 12288, 4096), ("down_q2k", ka.Q2K, 0, 4096, 12288),
+                     ("up_q3k", ka.Q3K, 0, 12288, 4096), ("down_q3k", ka.Q3K, 0, 4096, 12288),
+                     ("up_q5k", ka.Q5K, 0, 12288, 4096), ("down_q5k", ka.Q5K, 0, 4096, 12288),
+                     ("q_int4", ka.INT4, 32, 4096, 4096)]
+            for name, fmt, group, n, k in parts:
+                d = ka.quantize(fmt, group, values(500 + len(c5), n * k))
+                copies = max(2, int(1.2e9 // d.size))
+                ws5 = [ka.QuantizedTensor(torch.from_numpy(d).to(dev), fmt, group, n, k) for _ in range(copies)]
+                for rows in (1, 8):
+                    x5 = torch.from_numpy(synth.normal(5, rows * k, 1.0).reshape(rows, k)).to(dev)
+                    o5 = torch.empty((rows, n), device=dev)
+                    reserve([("w",)], {"w": ws5[0]}, rows, False)
+                    s5, _ = timed([(lambda w=w: hip.forward(op, [x5, w], out=o5)) for w in ws5], 4 * copies, copies)
+                    c5[f"{name}_m{rows}"] = {"us": round(s5 * 1e6, 2), "gbps": round(d.size / s5 / 1e9, 1)}
+                del ws5
+            table = ka.quantize(ka.Q6K, 0, values(77, 151936 * 4096))
+            wt = ka.QuantizedTensor(torch.from_numpy(table).to(dev), ka.Q6K, 0, 151936, 4096)
             for rows in (1, 8):
-                x5 = torch.from_numpy(synth.normal(5, rows * k, 1.0).reshape(rows, k)).to(dev)
-                o5 = torch.empty((rows, n), device=dev)
-                reserve([("w",)], {"w": ws5[0]}, rows, False)
-                s5, _ = timed([(lambda w=w: hip.forward(op, [x5, w], out=o5)) for w in ws5], 4 * copies, copies)
-                c5[f"{name}_m{rows}"] = {"us": round(s5 * 1e6, 2), "gbps": round(d.size / s5 / 1e9, 1)}
-            del ws5
-        table = ka.quantize(ka.Q6K, 0, values(77, 151936 * 4096))
-        wt = ka.QuantizedTensor(torch.from_numpy(table).to(dev), ka.Q6K, 0, 151936, 4096)
-        for rows in (1, 8):
-            xt = torch.from_numpy(synth.normal(6, rows * 4096, 1.0).reshape(rows, 4096)).to(dev)
-            ot = torch.empty((rows, 151936), device=dev)
-            reserve([("w",)], {"w": wt}, rows, False)
-            st, _ = timed([lambda: hip.forward(op, [xt, wt], out=ot)], 20, 4)
-            c5[f"table_q6k_m{rows}"] = {"us": round(st * 1e6, 2), "gbps": round(table.size / st / 1e9, 1)}
-        configs["5"] = {"workload": "Q2_K/Q3_K/Q5_K FFN (12288x4096, 4096x12288), int4/32 4096x4096, "
-                                    "Q6_K output table 151936x4096; f32 x; weights from 4 Mi N(0, 0.02) values repeated",
-                        "calls": c5}
-        del wt
+                xt = torch.from_numpy(synth.normal(6, rows * 4096, 1.0).reshape(rows, 4096)).to(dev)
+                ot = torch.empty((rows, 151936), device=dev)
+                reserve([("w",)], {"w": wt}, rows, False)
+                st, _ = timed([lambda: hip.forward(op, [xt, wt], out=ot)], 20, 4)
+                c5[f"table_q6k_m{rows}"] = {"us": round(st * 1e6, 2), "gbps": round(table.size / st / 1e9, 1)}
+            configs["5"] = {"workload": "Q2_K/Q3_K/Q5_K FFN (12288x4096, 4096x12288), int4/32 4096x4096, "
+                                        "Q6_K output table 151936x4096; f32 x; weights from 4 Mi N(0, 0.02) values repeated",
+                            "calls": c5}
+            del wt
 
-        # ---- config 4: Qwen3-8B layer, Q8_0, M = 512, bf16 activations in bytes
-        qhost, qbytes = quantized_layer(QWEN_LAYER, 300, lambda r: ka.Q8_0)
-        qlayers = [{name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
-                    for name, (fmt, data, n, k) in qhost.items()} for _ in range(2)]
-        hip.with_byte_activations(True)
-        reserve(QWEN_CALLS, qlayers[0], 512, True)
-        xq, oq = inputs_for(QWEN_CALLS, qhost, 512, dtype=torch.bfloat16)
+        if "4" in only:
+            # ---- config 4: Qwen3-8B layer, Q8_0, M = 512, bf16 activations in bytes
+            qhost, qbytes = quantized_layer(QWEN_LAYER, 300, lambda r: ka.Q8_0)
+            qlayers = [{name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
+                        for name, (fmt, data, n, k) in qhost.items()} for _ in range(2)]
+            hip.with_byte_activations(True)
+            reserve(QWEN_CALLS, qlayers[0], 512, True)
+            xq, oq = inputs_for(QWEN_CALLS, qhost, 512, dtype=torch.bfloat16)
 
-        def qwen_step(l):
-            def run():
-                for ci, call in enumerate(QWEN_CALLS):
-                    hip.forward(op, [xq[ci]] + [qlayers[l][c] for c in call], out=oq[ci])
-            return run
+            def qwen_step(l):
+                def run():
+                    for ci, call in enumerate(QWEN_CALLS):
+                        hip.forward(op, [xq[ci]] + [qlayers[l][c] for c in call], out=oq[ci])
+                return run
 
-        s4, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
-        hip.with_byte_activations(False)
-        ops4 = 2 * 512 * sum(n * k for _, n, k in QWEN_LAYER)
-        configs["4"] = {"workload": "Qwen3-8B layer in Q8_0, M = 512, bf16 activations quantized to bytes",
-                        "ms_per_step": round(s4 * 1e3, 3), "tops": round(ops4 / s4 / 1e12, 2),
-                        "mfma_frac": round(ops4 / s4 / 1e12 / INT8_PEAK_TOPS, 4),
-                        "weight_gbps": round(qbytes / s4 / 1e9, 1)}
-        del qlayers
+            s4, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
+            hip.with_byte_activations(False)
+            ops4 = 2 * 512 * sum(n * k for _, n, k in QWEN_LAYER)
+            configs["4"] = {"workload": "Qwen3-8B layer in Q8_0, M = 512, bf16 activations quantized to bytes",
+                            "ms_per_step": round(s4 * 1e3, 3), "tops": round(ops4 / s4 / 1e12, 2),
+                            "mfma_frac": round(ops4 / s4 / 1e12 / INT8_PEAK_TOPS, 4),
+                            "weight_gbps": round(qbytes / s4 / 1e9, 1)}
+            del qlayers
 
     cpu = None
     if not args.no_cpu:
