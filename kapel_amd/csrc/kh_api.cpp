@@ -97,6 +97,7 @@ Split split_k(uint64_t tiles, int steps, int rows, int planes, uint32_t fmt) {
 // rows it takes in one launch (in chunks of the former).
 int gemv_max_rows(int planes) { return planes == 1 ? 16 : 8; }
 constexpr uint64_t GEMV_ROWS = 64;
+constexpr int GEMV_DIRECT_ROWS = 4;
 
 // Its split, a function of the shapes only: tiles per workgroup (4, 2 or 1:
 // as many as still leave a workgroup for each of the 256 CUs), waves per tile
@@ -281,7 +282,9 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         bool offsets32 = true;
         for (uint32_t m : L.members) offsets32 = offsets32 && weights[m].bytes < (1ull << 31);
         L.mm = false;
-        bool one_chunk = rows <= (uint64_t)gemv_max_rows(planes);
+        // Up to four rows the small-M product; from five the many-row
+        // product is faster (measured across formats and shapes).
+        bool one_chunk = rows <= (uint64_t)std::min(GEMV_DIRECT_ROWS, gemv_max_rows(planes));
         if (unit && offsets32 && (one_chunk || (rows <= GEMV_ROWS && !mm_group(w.format, w.group)))) {
             L.gemv = true;
             L.r0 = 0;
