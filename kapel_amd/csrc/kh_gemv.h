@@ -619,60 +619,57 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
     const float4 *my_info = info + F::xpos(g, 0) / 32;
     const int blocks32 = a.k / 32;
 
-    for (int t = 0; t < T; t++) {
+    // One unit of one tile into acc.
+    auto unit = [&](int t, int jj, float (&acc)[ACC]) __attribute__((always_inline)) {
         int mat;
         const int64_t n = row_of(t0 + t, n16, mat);
-        // This tile's copies are the first ceil((t + 1) tchunks / 64).
-        wait_vm_n(TB - (((t + 1) * tchunks + 63) >> 6));
-        float acc[ACC];
+        const int u = cw + jj * a.kw;
+        const bool ok = U == 256 || 4 * u + g < blocks32;
+        const uint32_t at = (uint32_t)n * (uint32_t)a.row_bytes + UN::block(u) * F::BYTES;
+        typename F::Regs R;
+        F::load(R, lanes::LdsSrc{mine}, (uint32_t)((t * tchunks + (jj * 16 + n16) * CW) * 16) + (at & 3u),
+                UN::local(u), g);
+        float sc[NG], mn[NG];
+        F::scales(R, g, sc, mn);
+        v4i c[MT];
 #pragma unroll
-        for (int i = 0; i < ACC; i++) acc[i] = 0.0f;
-        for (int jj = 0; jj < upw; jj++) {
-            const int u = cw + jj * a.kw;
-            const bool ok = U == 256 || 4 * u + g < blocks32;
-            const uint32_t at = (uint32_t)n * (uint32_t)a.row_bytes + UN::block(u) * F::BYTES;
-            typename F::Regs R;
-            F::load(R, lanes::LdsSrc{mine}, (uint32_t)((t * tchunks + (jj * 16 + n16) * CW) * 16) + (at & 3u),
-                    UN::local(u), g);
-            float sc[NG], mn[NG];
-            F::scales(R, g, sc, mn);
-            v4i c[MT];
+        for (int s = 0; s < F::STEPS; s++) {
+            v4i bw = F::codes(R, s, g);
+            if (U == 128 && !ok) bw = v4i{0, 0, 0, 0};
+            if (F::GS == 16 || (s & 1) == 0)
 #pragma unroll
-            for (int s = 0; s < F::STEPS; s++) {
-                v4i bw = F::codes(R, s, g);
-                if (U == 128 && !ok) bw = v4i{0, 0, 0, 0};
-                if (F::GS == 16 || (s & 1) == 0)
+                for (int mi = 0; mi < MT; mi++) c[mi] = v4i{0, 0, 0, 0};
+            const int xo = u * U + F::xpos(g, s) - F::xpos(g, 0);
 #pragma unroll
-                    for (int mi = 0; mi < MT; mi++) c[mi] = v4i{0, 0, 0, 0};
-                const int xo = u * U + F::xpos(g, s) - F::xpos(g, 0);
+            for (int mi = 0; mi < MT; mi++) {
+                v4i av = *reinterpret_cast<const v4i *>(planes + a_off[mi] + xo);
+                c[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bw, c[mi], 0, 0, 0);
+            }
+            if (!(F::GS == 16 || (s & 1) == 1)) continue;
+            // The group of this step is complete: scale it (nothing past K).
+            const int s0 = F::GS == 16 ? s : s - 1, gi = F::GS == 16 ? s : s / 2;
+            const int blk = (u * U + F::xpos(g, s0) - F::xpos(g, 0)) / 32;
+            const bool second = ((F::xpos(g, s0) / 16) & 1) != 0;
 #pragma unroll
-                for (int mi = 0; mi < MT; mi++) {
-                    v4i av = *reinterpret_cast<const v4i *>(planes + a_off[mi] + xo);
-                    c[mi] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av, bw, c[mi], 0, 0, 0);
-                }
-                if (!ok || !(F::GS == 16 || (s & 1) == 1)) continue;
-                // The group of this step is complete: scale it.
-                const int s0 = F::GS == 16 ? s : s - 1, gi = F::GS == 16 ? s : s / 2;
-                const int blk = (u * U + F::xpos(g, s0) - F::xpos(g, 0)) / 32;
-                const bool second = ((F::xpos(g, s0) / 16) & 1) != 0;
+            for (int mi = 0; mi < MT; mi++) {
 #pragma unroll
-                for (int mi = 0; mi < MT; mi++) {
-#pragma unroll
-                    for (int j = 0; j < (P == 3 ? 1 : 4); j++) {
-                        int m = P == 3 ? mi : 4 * mi + j;
-                        if (m >= rows) continue;
-                        float4 in = my_info[(size_t)m * (span / 32) + blk];
-                        float dot;
-                        if (P == 3) dot = fmaf((float)c[mi].x, a.hi, (float)((c[mi].y << a.shift) + c[mi].z));
-                        else dot = (float)c[mi][j];
-                        float xsum = F::GS == 32 ? in.y : (second ? in.w : in.z);
-                        float tt = fmaf(dot, sc[gi] * in.x, acc[m]);
-                        acc[m] = fmaf(-mn[gi], xsum, tt);
-                    }
+                for (int j = 0; j < (P == 3 ? 1 : 4); j++) {
+                    int m = P == 3 ? mi : 4 * mi + j;
+                    if (m >= rows) continue;
+                    float4 in = my_info[(size_t)m * (span / 32) + (ok ? blk : 0)];
+                    float dot;
+                    if (P == 3) dot = fmaf((float)c[mi].x, a.hi, (float)((c[mi].y << a.shift) + c[mi].z));
+                    else dot = (float)c[mi][j];
+                    float xsum = F::GS == 32 ? in.y : (second ? in.w : in.z);
+                    float tt = fmaf(dot, sc[gi] * in.x, acc[m]);
+                    tt = fmaf(-mn[gi], xsum, tt);
+                    acc[m] = ok ? tt : acc[m];
                 }
             }
         }
-        // The four lane groups of each row in a fixed tree, then to LDS.
+    };
+    // The four lane groups of each row in a fixed tree, then to LDS.
+    auto finish = [&](int t, float (&acc)[ACC]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < ACC; i++) {
             float v = acc[i];
@@ -683,6 +680,55 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
 #pragma unroll
             for (int i = 0; i < ACC; i++)
                 if (i < rows) sums[((cw * a.tiles + t) * 16 + n16) * rows + i] = acc[i];
+    };
+    // Units two at a time, so that their LDS reads and MFMAs overlap: pairs
+    // of units of a tile (then their sums added), or, with one unit a wave,
+    // pairs of tiles.
+    if (upw >= 2) {
+        for (int t = 0; t < T; t++) {
+            // This tile's copies are the first ceil((t + 1) tchunks / 64).
+            wait_vm_n(TB - (((t + 1) * tchunks + 63) >> 6));
+            float acc[ACC], acc2[ACC];
+#pragma unroll
+            for (int i = 0; i < ACC; i++) acc[i] = acc2[i] = 0.0f;
+            int jj = 0;
+            for (; jj + 1 < upw; jj += 2) {
+                unit(t, jj, acc);
+                unit(t, jj + 1, acc2);
+            }
+            if (jj < upw) unit(t, jj, acc);
+#pragma unroll
+            for (int i = 0; i < ACC; i++) acc[i] = acc[i] + acc2[i];
+            finish(t, acc);
+        }
+    } else if (upw == 1) {
+        int t = 0;
+        for (; t + 1 < T; t += 2) {
+            wait_vm_n(TB - (((t + 2) * tchunks + 63) >> 6));
+            float acc[ACC], acc2[ACC];
+#pragma unroll
+            for (int i = 0; i < ACC; i++) acc[i] = acc2[i] = 0.0f;
+            unit(t, 0, acc);
+            unit(t + 1, 0, acc2);
+            finish(t, acc);
+            finish(t + 1, acc2);
+        }
+        if (t < T) {
+            wait_vm_n(TB - (((t + 1) * tchunks + 63) >> 6));
+            float acc[ACC];
+#pragma unroll
+            for (int i = 0; i < ACC; i++) acc[i] = 0.0f;
+            unit(t, 0, acc);
+            finish(t, acc);
+        }
+    } else {
+        // No unit for this wave (more waves than units): zero sums.
+        for (int t = 0; t < T; t++) {
+            float acc[ACC];
+#pragma unroll
+            for (int i = 0; i < ACC; i++) acc[i] = 0.0f;
+            finish(t, acc);
+        }
     }
     wait_vm_n(0);
     lds_barrier();  // the sums are written
