@@ -43,9 +43,9 @@ extern "C" {
 #define KH_Q4K 7u
 #define KH_Q5K 8u
 #define KH_Q6K 9u
-#define KH_IQ4_NL 10u /* reserved: not decoded by this library yet */
-#define KH_IQ4_XS 11u /* reserved */
-#define KH_IQ3_S 12u  /* reserved */
+#define KH_IQ4_NL 10u /* f32 activations only (bytes.rs:51-77 has no IQ) */
+#define KH_IQ4_XS 11u
+#define KH_IQ3_S 12u
 #define KH_Q2K 13u
 #define KH_Q3K 14u
 

@@ -29,7 +29,7 @@ IQ4_NL, IQ4_XS, IQ3_S = 10, 11, 12
 Q2K, Q3K = 13, 14
 FORMAT_NAMES = {INT8: "int8", INT4: "int4", Q8_0: "q8_0", Q4_0: "q4_0", Q4_1: "q4_1",
                 Q5_0: "q5_0", Q5_1: "q5_1", Q4K: "q4_k", Q5K: "q5_k", Q6K: "q6_k",
-                Q2K: "q2_k", Q3K: "q3_k"}
+                Q2K: "q2_k", Q3K: "q3_k", IQ4_NL: "iq4_nl", IQ4_XS: "iq4_xs", IQ3_S: "iq3_s"}
 # Float types (kapel-cuda-abi/src/lib.rs:152-163).
 F32, BF16, F16 = 0, 1, 2
 BYTE_ACTIVATIONS = 1

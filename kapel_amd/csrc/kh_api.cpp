@@ -593,8 +593,9 @@ uint32_t kh_block_len(uint32_t format, uint32_t group) {
     switch (format) {
     case KH_INT8: return group;
     case KH_INT4: return (group % 2 == 0) ? group : 0;
-    case KH_Q8_0: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1: return 32;
-    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: return 256;
+    case KH_Q8_0: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1: case KH_IQ4_NL: return 32;
+    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: case KH_IQ4_XS: case KH_IQ3_S:
+        return 256;
     default: return 0;
     }
 }
@@ -613,6 +614,9 @@ uint32_t kh_block_bytes(uint32_t format, uint32_t group) {
     case KH_Q4K: return 144;
     case KH_Q5K: return 176;
     case KH_Q6K: return 210;
+    case KH_IQ4_NL: return 18;
+    case KH_IQ4_XS: return 136;
+    case KH_IQ3_S: return 110;
     default: return 0;
     }
 }

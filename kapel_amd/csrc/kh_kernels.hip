@@ -26,6 +26,7 @@
 #include <stdint.h>
 
 #include "kh_formats.h"
+#include "kh_iq.h"
 #include "kh_internal.h"
 
 namespace kh {
@@ -503,6 +504,28 @@ __device__ float element(uint32_t fmt, uint32_t group, const uint8_t *row, uint6
         uint32_t qh = (blk[128 + h * 32 + l] >> (2 * s)) & 3u;
         float scale = half_at(blk + 208) * (float)(int8_t)blk[192 + f / 16];
         return scale * ((float)(ql | (qh << 4)) - 32.0f);
+    }
+    case KH_IQ4_NL: {
+        const uint8_t *blk = row + (e / 32) * 18;
+        uint32_t j = e % 32, byte = blk[2 + j % 16];
+        return half_at(blk) * (float)iq4nl_value(j < 16 ? byte & 15u : byte >> 4);
+    }
+    case KH_IQ4_XS: {
+        const uint8_t *blk = row + (e / 256) * 136;
+        uint32_t f = e % 256, g = f / 32, j = f % 32;
+        int s = (int)((blk[4 + g / 2] >> (4 * (g % 2))) & 15u) | (int)(((ld16(blk + 2) >> (2 * g)) & 3u) << 4);
+        uint32_t byte = blk[8 + 16 * g + j % 16];
+        float scale = half_at(blk) * (float)(s - 32);
+        return scale * (float)iq4nl_value(j < 16 ? byte & 15u : byte >> 4);
+    }
+    case KH_IQ3_S: {
+        const uint8_t *blk = row + (e / 256) * 110;
+        uint32_t f = e % 256, g = f / 32, l = f % 32 / 8, j = f % 8;
+        uint32_t s = (blk[106 + g / 2] >> (4 * (g % 2))) & 15u;
+        float db = half_at(blk) * (float)(1u + 2u * s);
+        uint32_t index = blk[2 + 8 * g + 2 * l + j / 4] | (((uint32_t)blk[66 + g] << (8 - 2 * l - j / 4)) & 256u);
+        float v = db * (float)((IQ3S_GRID[index] >> (8 * (j % 4))) & 255u);
+        return ((blk[74 + 4 * g + l] >> j) & 1u) ? -v : v;
     }
     default:
         return __uint_as_float(0x7fc00000u);  // unknown code: NaN, never a fault

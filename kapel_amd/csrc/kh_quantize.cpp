@@ -382,6 +382,8 @@ extern "C" int64_t kh_quantize_host(uint32_t format, uint32_t group, const float
                                      uint64_t count, uint8_t *out, int threads) {
     uint32_t len = kh_block_len(format, group), size = kh_block_bytes(format, group);
     if (len == 0 || size == 0) return -KH_ERR_DTYPE;
+    // The non-linear formats have no encoder (dtype.rs:547-556 writes none).
+    if (format == KH_IQ4_NL || format == KH_IQ4_XS || format == KH_IQ3_S) return -KH_ERR_DTYPE;
     if (count % len) return -KH_ERR_MISALIGNED;
     if (!values || !out) return count == 0 ? 0 : -KH_ERR_NULL;
     uint64_t blocks = count / len;

@@ -15,6 +15,7 @@ LIB_PATH = os.path.join(HERE, "libkapel_oracle.so")
 
 # Format codes of kapel-cuda-abi/src/lib.rs:167-194, plus Q2_K and Q3_K.
 INT8, INT4, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4K, Q5K, Q6K = range(10)
+IQ4_NL, IQ4_XS, IQ3_S = 10, 11, 12
 Q2K, Q3K = 13, 14
 
 _lib = None
@@ -45,6 +46,8 @@ def lib():
         L.ko_product_f64.argtypes = [i32, P, P, P, P, i64, P, i64, P]
         L.ko_quantize_x.argtypes = [P, i64, i64, P, P, P]
         L.ko_bytes_layout.argtypes = [i32, i32, P, P, P, P]
+        L.ko_iq_table.argtypes = [i32, i32]
+        L.ko_iq_table.restype = i64
         _lib = L
     return _lib
 
@@ -97,6 +100,11 @@ def quantize(fmt, group, values):
     n = lib().ko_quantize(fmt, group, _p(values), values.size, _p(out))
     assert n == out.size, n
     return out
+
+
+def iq_table(which, index):
+    """0: IQ4_NL's 16 values; 1: IQ3_S's grid of 512 (-1 past the end)."""
+    return lib().ko_iq_table(which, index)
 
 
 def decode_f32(fmt, group, block):

@@ -19,6 +19,7 @@ import oracle as ko  # noqa: E402
 from refrng import Rng, lcg_bytes  # noqa: E402
 
 INT8, INT4, Q8_0, Q4_0, Q4_1, Q5_0, Q5_1, Q4K, Q5K, Q6K = range(10)
+IQ4_NL, IQ4_XS, IQ3_S = 10, 11, 12
 Q2K, Q3K = 13, 14
 F32, BF16, F16 = 0, 1, 2
 
@@ -38,7 +39,7 @@ L.kh_quantize_x.argtypes = [u32, P, u64, u64, P, P, P, P]
 L.kh_dequantize.argtypes = [ctypes.POINTER(W), u64, u64, u64, u32, P, P]
 
 HALVES = {Q8_0: [0], Q4_0: [0], Q5_0: [0], Q4_1: [0, 2], Q5_1: [0, 2], Q4K: [0, 2], Q5K: [0, 2],
-          Q2K: [80, 82], Q3K: [108], Q6K: [208]}
+          Q2K: [80, 82], Q3K: [108], Q6K: [208], IQ4_NL: [0], IQ4_XS: [0], IQ3_S: [0]}
 FAILED = []
 
 
@@ -196,7 +197,7 @@ def case_dequantize(fmt, group):
 
 FORMATS = [(INT8, 32), (INT8, 64), (INT8, 40), (INT8, 128), (INT4, 32), (INT4, 64), (INT4, 128),
            (INT4, 40), (Q8_0, 0), (Q4_0, 0), (Q4_1, 0), (Q5_0, 0), (Q5_1, 0), (Q2K, 0), (Q3K, 0),
-           (Q4K, 0), (Q5K, 0), (Q6K, 0)]
+           (Q4K, 0), (Q5K, 0), (Q6K, 0), (IQ4_NL, 0), (IQ4_XS, 0), (IQ3_S, 0)]
 BYTE_FORMATS = [(Q8_0, 0), (Q4_0, 0), (Q4K, 0), (Q5K, 0), (Q6K, 0), (INT8, 32), (INT8, 128),
                 (INT4, 32), (INT4, 64)]
 

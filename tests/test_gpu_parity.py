@@ -40,7 +40,8 @@ def dev(a, dtype=None):
 
 
 HALVES = {ka.Q8_0: [0], ka.Q4_0: [0], ka.Q5_0: [0], ka.Q4_1: [0, 2], ka.Q5_1: [0, 2],
-          ka.Q4K: [0, 2], ka.Q5K: [0, 2], ka.Q2K: [80, 82], ka.Q3K: [108], ka.Q6K: [208]}
+          ka.Q4K: [0, 2], ka.Q5K: [0, 2], ka.Q2K: [80, 82], ka.Q3K: [108], ka.Q6K: [208],
+          ka.IQ4_NL: [0], ka.IQ4_XS: [0], ka.IQ3_S: [0]}
 
 
 def random_blocks(fmt, group, count, seed):
@@ -73,7 +74,7 @@ def x_uniform(rows, k, seed):
 FORMATS = [(ka.INT8, 32), (ka.INT8, 64), (ka.INT8, 40), (ka.INT8, 128), (ka.INT4, 32),
            (ka.INT4, 64), (ka.INT4, 128), (ka.INT4, 40), (ka.Q8_0, 0), (ka.Q4_0, 0), (ka.Q4_1, 0),
            (ka.Q5_0, 0), (ka.Q5_1, 0), (ka.Q2K, 0), (ka.Q3K, 0), (ka.Q4K, 0), (ka.Q5K, 0),
-           (ka.Q6K, 0)]
+           (ka.Q6K, 0), (ka.IQ4_NL, 0), (ka.IQ4_XS, 0), (ka.IQ3_S, 0)]
 
 
 def check_f32(got, e64, what):

@@ -34,7 +34,8 @@ def test_library_exports_every_declared_symbol():
 
 FORMATS = [(ka.INT8, 32), (ka.INT8, 40), (ka.INT8, 64), (ka.INT8, 128), (ka.INT4, 32),
            (ka.INT4, 40), (ka.INT4, 64), (ka.Q8_0, 0), (ka.Q4_0, 0), (ka.Q4_1, 0), (ka.Q5_0, 0),
-           (ka.Q5_1, 0), (ka.Q2K, 0), (ka.Q3K, 0), (ka.Q4K, 0), (ka.Q5K, 0), (ka.Q6K, 0)]
+           (ka.Q5_1, 0), (ka.Q2K, 0), (ka.Q3K, 0), (ka.Q4K, 0), (ka.Q5K, 0), (ka.Q6K, 0),
+           (ka.IQ4_NL, 0), (ka.IQ4_XS, 0), (ka.IQ3_S, 0)]
 
 
 @pytest.mark.parametrize("fmt,group", FORMATS)
@@ -44,7 +45,7 @@ def test_geometry_matches_the_oracle(fmt, group):
 
 
 def test_unknown_formats_have_no_geometry():
-    assert ka.block_len(99, 0) == 0 and ka.block_bytes(ka.IQ4_NL, 0) == 0
+    assert ka.block_len(99, 0) == 0 and ka.block_bytes(15, 0) == 0
     assert ka.block_len(ka.INT4, 7) == 0  # odd int4 groups (dtype.rs:119-128)
     assert ka.block_len(ka.INT8, 0) == 0
 

@@ -269,6 +269,120 @@ def test_golden_q6k():
     assert (got[0], got[15], got[16], got[255]) == (32.0, 32.0, -16.0, -16.0)
 
 
+# ------------------------------------------- the non-linear IQ formats ---
+# Their tables are format constants (ggml's kvalues_iq4nl and iq3s_grid);
+# tests/golden/iq_tables.json holds them as kapel-core/src/iq.rs:7-78 gives
+# them.  The transcriptions below follow GGML's dequantize_row_iq4_nl,
+# _iq4_xs and _iq3_s loops (a group of 32 at a time, pairs of groups for
+# IQ3_S), not the oracle's per-element formulas.
+
+def iq_tables():
+    import json
+    import os
+    with open(os.path.join(os.path.dirname(__file__), "golden", "iq_tables.json")) as f:
+        t = json.load(f)
+    return t["iq4nl_values"], t["iq3s_grid"]
+
+
+def test_iq_tables_are_the_formats_tables():
+    values, grid = iq_tables()
+    # What the formats fix: 16 increasing values of a signed byte; 512
+    # distinct groups of four odd magnitudes 1..15 (3 bits each).
+    assert len(values) == 16 and all(a < b for a, b in zip(values, values[1:]))
+    assert values[0] == -127 and values[-1] == 113
+    assert len(grid) == 512 and len(set(grid)) == 512
+    for g in grid:
+        for j in range(4):
+            m = (g >> (8 * j)) & 0xFF
+            assert m % 2 == 1 and 1 <= m <= 15
+    # The oracle holds the same tables.
+    assert [ko.iq_table(0, i) for i in range(16)] == values
+    assert [ko.iq_table(1, i) for i in range(512)] == grid
+    assert ko.iq_table(0, 16) == -1 and ko.iq_table(1, 512) == -1
+
+
+def ggml_iq4_nl(data, d):
+    values, _ = iq_tables()
+    qs = data[2:18]
+    y = [0.0] * 32
+    for j in range(16):
+        y[j] = d * values[qs[j] & 0xF]
+        y[j + 16] = d * values[qs[j] >> 4]
+    return y
+
+
+def ggml_iq4_xs(data, d):
+    values, _ = iq_tables()
+    scales_h = int(data[2]) | int(data[3]) << 8
+    scales_l, qs = data[4:8], data[8:136]
+    y = []
+    for ib in range(8):
+        ls = ((int(scales_l[ib // 2]) >> 4 * (ib % 2)) & 0xF) | ((scales_h >> 2 * ib) & 3) << 4
+        dl = d * (ls - 32)
+        q = qs[16 * ib:16 * ib + 16]
+        y += [dl * values[q[j] & 0xF] for j in range(16)]
+        y += [dl * values[q[j] >> 4] for j in range(16)]
+    return y
+
+
+def ggml_iq3_s(data, d):
+    _, grid = iq_tables()
+    qs, qh, signs, scales = data[2:66], data[66:74], data[74:106], data[106:110]
+    y = []
+    q, s, h = 0, 0, 0
+    for ib32 in range(0, 8, 2):
+        for half in range(2):
+            db = d * (1 + 2 * ((int(scales[ib32 // 2]) >> 4 * half) & 0xF))
+            for l in range(4):
+                g1 = grid[int(qs[q + 2 * l]) | ((int(qh[h + half]) << (8 - 2 * l)) & 256)]
+                g2 = grid[int(qs[q + 2 * l + 1]) | ((int(qh[h + half]) << (7 - 2 * l)) & 256)]
+                sg = int(signs[s + l])
+                for j in range(4):
+                    y.append(db * ((g1 >> 8 * j) & 0xFF) * (-1.0 if sg & (1 << j) else 1.0))
+                for j in range(4):
+                    y.append(db * ((g2 >> 8 * j) & 0xFF) * (-1.0 if sg & (1 << (j + 4)) else 1.0))
+            q += 8
+            s += 4
+        h += 2
+    return y
+
+
+def test_golden_iq4_nl():
+    data = golden_block(18, 9, [(0, HALF)])
+    same(ko.dequantize(ko.IQ4_NL, 0, data), ggml_iq4_nl(data, 0.5))
+    by_hand = np.array([0x00, 0x3C, 0xF0] + [0x87] * 15, dtype=np.uint8)
+    got = ko.dequantize(ko.IQ4_NL, 0, by_hand)
+    assert (got[0], got[16], got[1], got[17]) == (-127.0, 113.0, -10.0, 1.0)
+
+
+def test_golden_iq4_xs():
+    data = golden_block(136, 10, [(0, QUARTER)])
+    same(ko.dequantize(ko.IQ4_XS, 0, data), ggml_iq4_xs(data, 0.25))
+    by_hand = np.zeros(136, dtype=np.uint8)
+    by_hand[0:2] = [0x00, 0x3C]          # d = 1
+    by_hand[2:4] = [0x02, 0xC0]          # group 0: high bits 2; group 7: 3
+    by_hand[4:8] = [0x01, 0, 0, 0xF0]    # group 0: low 1 -> s = 33; group 7: 15 | 48 = 63
+    by_hand[8] = 0x0F                    # element 0: code 15, element 16: code 0
+    got = ko.dequantize(ko.IQ4_XS, 0, by_hand)
+    assert (got[0], got[16], got[1]) == (113.0, -127.0, -127.0)
+    assert got[224] == 31.0 * -127.0 and got[32] == -32.0 * -127.0
+
+
+def test_golden_iq3_s():
+    data = golden_block(110, 11, [(0, HALF)])
+    same(ko.dequantize(ko.IQ3_S, 0, data), ggml_iq3_s(data, 0.5))
+    _, grid = iq_tables()
+    by_hand = np.zeros(110, dtype=np.uint8)
+    by_hand[0:2] = [0x00, 0x3C]          # d = 1
+    by_hand[66] = 0x01                   # group 0, first index: + 256
+    by_hand[74] = 0x01                   # element 0 negative
+    by_hand[106] = 0x20                  # group 1: s = 2, scale 5
+    got = ko.dequantize(ko.IQ3_S, 0, by_hand)
+    first = [(grid[256] >> 8 * j) & 0xFF for j in range(4)]
+    assert list(got[:4]) == [-first[0], first[1], first[2], first[3]]
+    assert list(got[4:8]) == [1.0] * 4 and list(got[32:36]) == [5.0] * 4
+
+
 # ----------------------------------------------------- dtype.rs tests ---
 
 def test_kapel_formats_dequantize():
@@ -292,7 +406,8 @@ def test_geometry():
     assert ko.block_len(ko.INT4, 64) * 2 == 128 and ko.block_bytes(ko.INT4, 64) == 36
     assert 512 // ko.block_len(ko.Q4K) * ko.block_bytes(ko.Q4K) == 288
     sizes = {ko.Q8_0: 34, ko.Q4_0: 18, ko.Q4_1: 20, ko.Q5_0: 22, ko.Q5_1: 24, ko.Q2K: 84,
-             ko.Q3K: 110, ko.Q4K: 144, ko.Q5K: 176, ko.Q6K: 210}
+             ko.Q3K: 110, ko.Q4K: 144, ko.Q5K: 176, ko.Q6K: 210, ko.IQ4_NL: 18,
+             ko.IQ4_XS: 136, ko.IQ3_S: 110}
     for fmt, size in sizes.items():
         assert ko.block_bytes(fmt) == size
 
@@ -353,10 +468,12 @@ def test_quantizer_hand_cases():
 
 FORMATS = [(ko.INT8, 32), (ko.INT8, 40), (ko.INT4, 64), (ko.INT4, 40), (ko.Q8_0, 0),
            (ko.Q4_0, 0), (ko.Q4_1, 0), (ko.Q5_0, 0), (ko.Q5_1, 0), (ko.Q2K, 0), (ko.Q3K, 0),
-           (ko.Q4K, 0), (ko.Q5K, 0), (ko.Q6K, 0)]
+           (ko.Q4K, 0), (ko.Q5K, 0), (ko.Q6K, 0), (ko.IQ4_NL, 0), (ko.IQ4_XS, 0),
+           (ko.IQ3_S, 0)]
 
 HALVES = {ko.Q8_0: [0], ko.Q4_0: [0], ko.Q5_0: [0], ko.Q4_1: [0, 2], ko.Q5_1: [0, 2],
-          ko.Q4K: [0, 2], ko.Q5K: [0, 2], ko.Q2K: [80, 82], ko.Q3K: [108], ko.Q6K: [208]}
+          ko.Q4K: [0, 2], ko.Q5K: [0, 2], ko.Q2K: [80, 82], ko.Q3K: [108], ko.Q6K: [208],
+          ko.IQ4_NL: [0], ko.IQ4_XS: [0], ko.IQ3_S: [0]}
 
 
 def lcg_blocks(fmt, group, count, seed):
@@ -553,7 +670,7 @@ def test_golden_fixture_matches_the_oracle():
     import os
     with open(os.path.join(os.path.dirname(__file__), "golden", "golden_blocks.json")) as f:
         cases = json.load(f)
-    assert len(cases) == 8
+    assert len(cases) == 11
     for case in cases:
         data = np.frombuffer(bytes.fromhex(case["bytes"]), dtype=np.uint8)
         same(ko.dequantize(case["format"], 0, data), case["values"])
