@@ -39,10 +39,12 @@ def build(verbose=False):
         ("kh_gemv_k.hip", HIPCC, HIP_FLAGS),
         ("kh_gemv_b.hip", HIPCC, HIP_FLAGS),
         ("kh_gemv_i.hip", HIPCC, HIP_FLAGS),
+        ("kh_gemv_q.hip", HIPCC, HIP_FLAGS),
         ("kh_mm.hip", HIPCC, HIP_FLAGS),
         ("kh_mm_k.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_mm_b.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_mm_i.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
+        ("kh_mm_q.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_api.cpp", HIPCC, HIP_FLAGS),
         ("kh_quantize.cpp", "g++", HOST_FLAGS),
     )

@@ -27,12 +27,22 @@ bool mfma_format(uint32_t fmt, uint32_t group) {
     switch (fmt) {
     case KH_Q8_0: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1:
     case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K:
+    case KH_IQ4_NL: case KH_IQ4_XS: case KH_IQ3_S:
         return true;
     case KH_INT8: case KH_INT4:
         return group == 32 || group == 64 || group == 128 || group == 256;
     default:
         return false;
     }
+}
+
+// Weights the generic kernel takes: formats without an MFMA reader, and the
+// non-linear formats in matrices of 2 GiB or more (read by the small-M and
+// many-row kernels only, at 32-bit offsets).
+bool generic_weight(const kh_weight &w) {
+    if (!mfma_format(w.format, w.group)) return true;
+    const bool iq = w.format == KH_IQ4_NL || w.format == KH_IQ4_XS || w.format == KH_IQ3_S;
+    return iq && w.bytes >= (1ull << 31);
 }
 
 // bytes.rs:51-77: the formats read with activations in bytes.
@@ -180,12 +190,14 @@ Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     const int cw = (ub + (bytes % 4 ? 2 : 0) + 15) / 16;
     const int units = (int)div_up(k, unit);
     const int quads = rows * units * unit / 4;
+    // IQ3_S's kernels keep a 2 KiB copy of its grid in LDS.
+    const size_t limit = 160 * 1024 - (fmt == KH_IQ3_S ? 2048 : 0);
     p.npw = std::max(1, std::min(4, (int)div_up(quads, 512)));
     for (int t = tiles; t >= 1; t /= 2)
         for (int kw = std::min(16 - p.npw, units); kw >= 1; kw--) {
             const int upw = (int)div_up(units, kw);
             const int tb = (int)div_up(t * 16 * cw * upw, 64);
-            if (gemv2_lds(rows, planes, units, unit, t, kw, tb) <= 160 * 1024) {
+            if (gemv2_lds(rows, planes, units, unit, t, kw, tb) <= limit) {
                 p.ok = true;
                 p.tiles = t;
                 p.kw = kw;
@@ -263,13 +275,14 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
     for (uint32_t i = 0; i < count; i++) {
         if (done[i]) continue;
         const kh_weight &w = weights[i];
-        if (!mfma_format(w.format, w.group)) {
+        if (generic_weight(w)) {
             done[i] = true;
             continue;
         }
         Launch L;
         for (uint32_t j = i; j < count && (int)L.members.size() < MAX_WEIGHTS; j++)
-            if (!done[j] && weights[j].format == w.format && weights[j].group == w.group) {
+            if (!done[j] && weights[j].format == w.format && weights[j].group == w.group &&
+                !generic_weight(weights[j])) {
                 L.members.push_back(j);
                 done[j] = true;
             }
@@ -406,7 +419,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     }
     for (uint32_t i = 0; i < count; i++) {
         const kh_weight &w = weights[i];
-        if (mfma_format(w.format, w.group) || w.n == 0) continue;
+        if (!generic_weight(w) || w.n == 0) continue;
         GenericArgs g{};
         g.format = w.format;
         g.group = w.group;

@@ -231,6 +231,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     const int mc = local % a.mchunks;
     const int group = (local / a.mchunks) * XCDS + b % XCDS;
     if (group * a.tiles >= a.total_tiles) return;
+    grid_fill<F>();
     const int m0 = mc * a.rows;
     const int rows = min(a.rows, a.rows_total - m0);
     const XIn xin{static_cast<const uint8_t *>(a.x) + (size_t)m0 * a.k * (XK == X_F32 ? 4 : XK == X_H16 ? 2 : 1),
@@ -528,6 +529,7 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
     const int group = blockIdx.x;
     const int t0 = group * a.tiles;
     if (t0 >= a.total_tiles) return;
+    grid_fill<F>();
     const int T = min(a.tiles, a.total_tiles - t0);
     const int rows = a.rows;
     const int lane = threadIdx.x & 63;
@@ -741,7 +743,8 @@ hipError_t launch2(const GemvArgs &a, hipStream_t s, size_t lds) {
     static bool ready = false;
     if (!ready) {
         hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv2_kernel<F, P, MT, XK>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+                                           hipFuncAttributeMaxDynamicSharedMemorySize,
+                                           160 * 1024 - grid_lds<F>());
         if (e != hipSuccess) return e;
         ready = true;
     }
@@ -757,7 +760,7 @@ hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
         if (a.tb * 64 < a.tiles * 16 * Unit<F>::CW * ((a.units + a.kw - 1) / a.kw) || a.npw + a.kw > 16)
             return hipErrorInvalidValue;
         size_t lds = gemv2_lds(a.rows, P, a.units, F::U, a.tiles, a.kw, a.tb);
-        if (lds > 160 * 1024) return hipErrorInvalidValue;
+        if (lds > (size_t)(160 * 1024 - grid_lds<F>())) return hipErrorInvalidValue;
         if (mt <= 1) return launch2<F, P, 1, XK>(a, s, lds);
         return hipErrorInvalidValue;
     }

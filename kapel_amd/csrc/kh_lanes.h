@@ -22,6 +22,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kh_iq.h"
+
 namespace kh {
 namespace lanes {
 
@@ -498,6 +500,109 @@ struct Int4G {
     __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
         sc[0] = __uint_as_float(r.scale);
         mn[0] = 8.0f * sc[0];
+    }
+};
+
+
+// ------------------------------------------------- the non-linear formats
+// Codes become their signed values (kh_iq.h); no minimum.  f32 activations
+// only: the byte mode has no reader for them (bytes.rs:51-77).
+__device__ __forceinline__ v4i iq4_vec(const uint32_t *q, int s) {
+    v4i c;
+    for (int i = 0; i < 4; i++) c[i] = (int)iq4_bytes(s ? (q[i] >> 4) & LO4 : q[i] & LO4);
+    return c;
+}
+
+// IQ4_NL: 18 bytes, d then 16 bytes of codes as Q4_0's (quantized.rs:420-433).
+struct IQ4NL {
+    static constexpr int U = 128, STEPS = 2, GS = 32, BYTES = 18, BLEN = 32;
+    struct Regs {
+        uint32_t w[5];
+    };
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
+        run<18>(r.w, src, row + (4 * u + g) * BYTES);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        uint32_t q[4];
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(r.w[i + 1], r.w[i], 2);
+        return iq4_vec(q, s);
+    }
+    __device__ static int xpos(int g, int s) { return 32 * g + 16 * s; }
+    __device__ static void scales(const Regs &r, int, float (&sc)[1], float (&mn)[1]) {
+        sc[0] = f16(r.w[0] & 0xffffu);
+        mn[0] = 0.0f;
+    }
+};
+
+// IQ4_XS: 136 bytes (quantized.rs:435-452): d, 16 high scale bits, 4 bytes of
+// low scale nibbles, then group G's 16 bytes at 8 + 16G (element 32G + j:
+// low nibble of byte j, 32G + 16 + j: high nibble); scale d (s - 32).  Lane
+// group g takes groups 2g (steps 0, 1) and 2g + 1 (steps 2, 3).
+struct IQ4XS {
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 136, BLEN = 256;
+    struct Regs {
+        uint32_t h[2], q[8];
+    };
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
+        ldb<2>(r.h, src, b);
+        ldb<8>(r.q, src, b + 8 + 32 * g);
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) { return iq4_vec(r.q + 4 * (s >> 1), s & 1); }
+    __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
+    __device__ static void scales(const Regs &r, int g, float (&sc)[2], float (&mn)[2]) {
+        const float d = f16(r.h[0] & 0xffffu);
+        for (int i = 0; i < 2; i++) {
+            const int G = 2 * g + i;
+            const int s = (int)((byte_of(r.h[1], g) >> (4 * i)) & 15u) | (int)(((r.h[0] >> (16 + 2 * G)) & 3u) << 4);
+            sc[i] = d * (float)(s - 32);
+            mn[i] = 0.0f;
+        }
+    }
+};
+
+// IQ3_S: 110 bytes (quantized.rs:454-485): d; 64 index bytes (group G's 8 at
+// 2 + 8G); 8 bytes of ninth index bits (byte G, bit i for index i); 32 sign
+// bytes (group G's 4 at 74 + 4G, byte l for elements 8l .. 8l + 7); 4 scale
+// bytes (nibble G of 106: scale d (1 + 2s)).  Lane group g takes groups 2g
+// and 2g + 1 as IQ4_XS; step s is dword s of its 16 index bytes: indices
+// 4(s % 2) .. + 3 of group 2g + s / 2, 16 elements.
+struct IQ3S {
+    static constexpr int U = 256, STEPS = 4, GS = 32, BYTES = 110, BLEN = 256;
+    static constexpr bool GRID = true;
+    struct Regs {
+        uint32_t c[4], hs, sg[2], sc, d;
+    };
+    template <class S>
+    __device__ static void load(Regs &r, const S &src, uint32_t row, int u, int g) {
+        const uint32_t b = row + u * BYTES;
+        uint32_t t[1];
+        run<16>(r.c, src, b + 2 + 16 * g);
+        run<2>(t, src, b + 66 + 2 * g);
+        r.hs = t[0] & 0xffffu;
+        run<8>(r.sg, src, b + 74 + 8 * g);
+        run<4>(t, src, b + 106);
+        r.sc = byte_of(t[0], g);
+        run<2>(t, src, b);
+        r.d = t[0] & 0xffffu;
+    }
+    __device__ static v4i codes(const Regs &r, int s, int) {
+        const uint32_t q = r.c[s], hb = byte_of(r.hs, s >> 1) >> (4 * (s & 1));
+        const uint32_t sg = r.sg[s >> 1] >> (16 * (s & 1));
+        v4i c;
+        for (int i = 0; i < 4; i++)
+            c[i] = (int)iq3s_bytes(byte_of(q, i) | (((hb >> i) & 1u) << 8), (sg >> (4 * i)) & 15u);
+        return c;
+    }
+    __device__ static int xpos(int g, int s) { return 64 * g + 16 * s; }
+    __device__ static void scales(const Regs &r, int, float (&sc)[2], float (&mn)[2]) {
+        const float d = f16(r.d);
+        for (int i = 0; i < 2; i++) {
+            sc[i] = d * (float)(1u + 2u * ((r.sc >> (4 * i)) & 15u));
+            mn[i] = 0.0f;
+        }
     }
 };
 

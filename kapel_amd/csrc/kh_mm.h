@@ -449,6 +449,104 @@ struct Int4G {
     }
 };
 
+// ------------------------------------------------- the non-linear formats
+// Codes become their signed values (kh_iq.h); no minimum; f32 activations
+// only (bytes.rs:51-77 has no byte reader for them).
+__device__ __forceinline__ v4i iq4_nibbles(const uint32_t *q, int h) {
+    v4i c;
+#pragma unroll
+    for (int i = 0; i < 4; i++) c[i] = (int)iq4_bytes(h ? (q[i] >> 4) & LO4 : q[i] & LO4);
+    return c;
+}
+
+// IQ4_NL: d, 16 bytes of codes as Q4_0's.
+struct IQ4NL {
+    static constexpr int U = 128, G = 32, NG = 4, BYTES = 18, BLEN = 32;
+    static constexpr bool MIN = false;
+    struct Regs {
+        uint32_t w[4][5];
+    };
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) rn<18>(r.w[j], s, row + (4 * u + j) * BYTES);
+    }
+    __device__ static v4i codes(const Regs &r, int j, int h) {
+        uint32_t q[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) q[i] = __builtin_amdgcn_alignbyte(r.w[j][i + 1], r.w[j][i], 2);
+        return iq4_nibbles(q, h);
+    }
+    __device__ static void scales(const Regs &r, float (&sc)[NG], float (&)[NG]) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) sc[j] = f16(r.w[j][0] & 0xffffu);
+    }
+};
+
+// IQ4_XS: d, 16 high scale bits, 4 bytes of low scale nibbles, group j's 16
+// code bytes at 8 + 16j (half h: nibble h of each); scale d (s - 32).
+struct IQ4XS {
+    static constexpr int U = 256, G = 32, NG = 8, BYTES = 136, BLEN = 256;
+    static constexpr bool MIN = false;
+    struct Regs {
+        uint32_t h[2], q[8][4];
+    };
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+        const uint32_t b = row + u * BYTES;
+        ld<2>(r.h, s, b);
+#pragma unroll
+        for (int j = 0; j < 8; j++) ld<4>(r.q[j], s, b + 8 + 16 * j);
+    }
+    __device__ static v4i codes(const Regs &r, int j, int h) { return iq4_nibbles(r.q[j], h); }
+    __device__ static void scales(const Regs &r, float (&sc)[NG], float (&)[NG]) {
+        const float d = f16(r.h[0] & 0xffffu);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int s = (int)((lanes::byte_of(r.h[1], j >> 1) >> (4 * (j & 1))) & 15u) |
+                          (int)(((r.h[0] >> (16 + 2 * j)) & 3u) << 4);
+            sc[j] = d * (float)(s - 32);
+        }
+    }
+};
+
+// IQ3_S: d; group j's 8 index bytes at 2 + 8j (half h: bytes 4h .. 4h + 3,
+// ninth bits 4h .. 4h + 3 of byte 66 + j); its 4 sign bytes at 74 + 4j (half
+// h: bytes 2h, 2h + 1); scale nibble j of 106: d (1 + 2s).
+struct IQ3S {
+    static constexpr int U = 256, G = 32, NG = 8, BYTES = 110, BLEN = 256;
+    static constexpr bool MIN = false, GRID = true;
+    struct Regs {
+        uint32_t c[8], hi[2], sg[8], sc, d;
+    };
+    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+        const uint32_t b = row + u * BYTES;
+        uint32_t t[1];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            rn<4>(t, s, b + 2 + 8 * j + 4 * h);
+            r.c[j] = t[0];
+        }
+        rn<8>(r.hi, s, b + 66);
+        rn<32>(r.sg, s, b + 74);
+        rn<4>(t, s, b + 106);
+        r.sc = t[0];
+        rn<2>(t, s, b);
+        r.d = t[0] & 0xffffu;
+    }
+    __device__ static v4i codes(const Regs &r, int j, int h) {
+        const uint32_t hb = lanes::byte_of(r.hi[j >> 2], j & 3) >> (4 * h), sg = r.sg[j] >> (16 * h);
+        v4i c;
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+            c[i] = (int)iq3s_bytes(lanes::byte_of(r.c[j], i) | (((hb >> i) & 1u) << 8), (sg >> (4 * i)) & 15u);
+        return c;
+    }
+    __device__ static void scales(const Regs &r, float (&sc)[NG], float (&)[NG]) {
+        const float d = f16(r.d);
+#pragma unroll
+        for (int j = 0; j < 8; j++) sc[j] = d * (float)(1u + 2u * ((lanes::byte_of(r.sc, j >> 1) >> (4 * (j & 1))) & 15u));
+    }
+};
+
 // ---------------------------------------------------------- the kernel
 constexpr int LDS_MAX = 160 * 1024;      // LDS of a CU (gfx950)
 
@@ -478,19 +576,21 @@ struct Plan {
     static constexpr int OA = 0, OW = IA * 1024, OS = OW + IW * 1024, OX = OS + IS * 256;
     static constexpr int SB = OX + IX * 256;
     static constexpr int D = (IA + IW + IS + IX) / WAVES;  // instructions a wave issues a stage
-    static constexpr int STAGES = 3 * SB <= LDS_MAX ? 3 : 2;
-    static constexpr bool FITS = 2 * SB <= LDS_MAX;
+    static constexpr int STAGES = 3 * SB + grid_lds<F>() <= LDS_MAX ? 3 : 2;
+    static constexpr bool FITS = 2 * SB + grid_lds<F>() <= LDS_MAX;
     static_assert(D * (STAGES - 2) <= 63, "the later stages' loads fit vmcnt");
     // The position of chunk o of activation row r.
     static constexpr int swz(int r) { return U == 128 ? (r >> 1) & 7 : r & 15; }
 };
 
-// Weight tiles of a wave: two, or one for the formats with a minimum term or
-// more than 24 dwords of a unit's lane bytes (their registers would not fit
-// two waves a SIMD) and where two stages of two would not fit in LDS.
+// Weight tiles of a wave: two with byte activations, or one for three planes
+// (their three dot sums a tile do not leave room for a second tile without
+// spills), for the formats with a minimum term or more than 24 dwords of a
+// unit's lane bytes (their registers would not fit two waves a SIMD) and
+// where two stages of two would not fit in LDS.
 template <class F, int P, int WM, int WMG>
 constexpr int wn_of() {
-    return !F::MIN && sizeof(typename F::Regs) <= 96 && Plan<F, P, WM, WMG, 2>::FITS ? 2 : 1;
+    return P == 1 && !F::MIN && sizeof(typename F::Regs) <= 96 && Plan<F, P, WM, WMG, 2>::FITS ? 2 : 1;
 }
 
 // An empty asm through which a value must pass (its order among the others
@@ -535,6 +635,7 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
     const int mt = local % a.mtiles;
     const int rest = (local / a.mtiles) * XCDS + b % XCDS;
     if (rest >= a.ngroups * a.ks) return;
+    grid_fill<F>();
     const int kz = rest / a.ngroups, ng = rest % a.ngroups;
     const int u0 = kz * a.ups, u1 = min(a.units, u0 + a.ups);
     const int m0 = mt * RM;
@@ -850,6 +951,17 @@ hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s, int *cols) {
     if (planes == 1) return launch_fp<F, 1>(a, s);
     if (planes == 3) return launch_fp<F, 3>(a, s);
     return hipErrorInvalidValue;
+}
+
+// The formats read with f32 activations only.
+template <class F>
+hipError_t launch_f3(const MmArgs &a, int planes, hipStream_t s, int *cols) {
+    if (planes != 3) return hipErrorInvalidValue;
+    if (cols) {
+        *cols = cols_f<F>(planes, a.wm, a.wmg);
+        return hipSuccess;
+    }
+    return launch_fp<F, 3>(a, s);
 }
 
 }  // namespace mm

@@ -1,6 +1,6 @@
 // The many-row product's entry points: the kernel of each format and the
 // reduction of K splits.  The kernels are in kh_mm.h, instantiated by format
-// family in kh_mm_k.hip, kh_mm_b.hip and kh_mm_i.hip.
+// family in kh_mm_k.hip, kh_mm_b.hip, kh_mm_i.hip and kh_mm_q.hip.
 #include "kh_mm.h"
 
 namespace kh {
@@ -24,11 +24,13 @@ __global__ void mm_reduce_kernel(MmArgs a) {
 hipError_t mm_kquants(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s, int *cols);
 hipError_t mm_blocks(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s, int *cols);
 hipError_t mm_groups(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s, int *cols);
+hipError_t mm_iq(uint32_t fmt, int planes, const MmArgs &a, hipStream_t s, int *cols);
 
 int mm_group(uint32_t fmt, uint32_t group) {
     switch (fmt) {
     case KH_Q2K: case KH_Q3K: case KH_Q6K: return 16;
     case KH_Q4K: case KH_Q5K: case KH_Q4_0: case KH_Q4_1: case KH_Q5_0: case KH_Q5_1: case KH_Q8_0:
+    case KH_IQ4_NL: case KH_IQ4_XS: case KH_IQ3_S:
         return 32;
     case KH_INT8: case KH_INT4:
         return (group == 32 || group == 64 || group == 128 || group == 256) ? 32 : 0;
@@ -45,6 +47,8 @@ hipError_t dispatch(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, h
         return mm_blocks(fmt, planes, a, s, cols);
     case KH_INT8: case KH_INT4:
         return mm_groups(fmt, group, planes, a, s, cols);
+    case KH_IQ4_NL: case KH_IQ4_XS: case KH_IQ3_S:
+        return mm_iq(fmt, planes, a, s, cols);
     }
     return hipErrorInvalidValue;
 }
@@ -65,7 +69,8 @@ int mm_cols(uint32_t fmt, uint32_t group, int planes, int rows) {
 
 int mm_unit(uint32_t fmt, uint32_t group) {
     switch (fmt) {
-    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: return 256;
+    case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K: case KH_IQ4_XS: case KH_IQ3_S:
+        return 256;
     case KH_INT8: case KH_INT4: return group == 256 ? 256 : 128;
     default: return 128;
     }

@@ -232,6 +232,14 @@ def main(which):
     case_product(Q4_0, 0, 20, 96, 33)       # a unit past K (96 = 3 blocks)
     case_product(Q5_1, 0, 20, 160, 9)       # minimums of the 32-element blocks
     case_bytes(INT4, 32, 20, 160, 24, dots=False)
+    # The non-linear formats: decode kernels (1, 3 rows), many rows, a unit
+    # past K for IQ4_NL.
+    case_product(IQ3_S, 0, 40, 512, 3)
+    case_product(IQ4_XS, 0, 40, 512, 3)
+    case_product(IQ4_NL, 0, 20, 160, 3)
+    case_product(IQ3_S, 0, 300, 1024, 40)
+    case_product(IQ4_XS, 0, 130, 512, 20)
+    case_product(IQ4_NL, 0, 20, 96, 9)
     k = 512
     parts = [(Q4K, 0, blocks(Q4K, 0, n * k // 256, 60 + i), n) for i, n in enumerate((260, 7))]
     x = xs(21, k, 5)
