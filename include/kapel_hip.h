@@ -18,6 +18,9 @@
  *   kh_dequantize    kernels/src/lib.rs:3745-3766 (dequantize)
  *   kh_dequantize_rows kernels/src/lib.rs:3773-3792 (dequantize_rows),
  *                    kapel-cuda/src/quantized.rs:358-386
+ *   kh_expert_matmul kapel-ops/src/experts.rs:130-229 (ExpertMatmul),
+ *                    kapel-cuda/src/experts.rs:127-250, kernels/src/lib.rs:3507-3681
+ *                    (expert_gemv, expert_gemv_bytes)
  *   kh_quantize_host kapel-core/src/dtype.rs:751-782 (quantize)
  *   kh_block_len/... kapel-core/src/dtype.rs:140-213
  */
@@ -142,6 +145,28 @@ int kh_dequantize(const kh_weight *weight, uint64_t k, uint64_t first, uint64_t 
  * out [count, k] = dequantized rows indices[0..count] (u32, device). */
 int kh_dequantize_rows(const kh_weight *weight, uint64_t k, const uint32_t *indices,
                        uint64_t count, uint32_t out_kind, void *out, void *stream);
+
+/* The product of each token by its experts (mixtures of experts).  weight:
+ * the experts' matrices stacked, [experts * n, k] (expert e: rows e n ..
+ * (e + 1) n); x [tokens, k] (per_route 0) or [tokens, topk, k] (per_route
+ * 1), contiguous on the device; idx [tokens * topk] u32 on the device, each
+ * token's experts; out [tokens, topk, n] in `out_kind`:
+ *     out[t, j, i] = sum_c x[t, (j,) c] w[idx[t, j] n + i, c].
+ * An index of `experts` or more gives NaN outputs for its route (the device
+ * never faults; kernels/src/lib.rs:3499-3504).  Flags: KH_BYTE_ACTIVATIONS
+ * as for kh_qmatmul.  The workspace (kh_expert_matmul_workspace bytes,
+ * 256-byte aligned) is used only when x is not 16-byte aligned (f32) or
+ * 8-byte aligned (16-bit).
+ * Replaces: ExpertMatmul (kapel-ops/src/experts.rs:130-229) with
+ * Cuda's expert_gemv / expert_gemv_bytes (kapel-cuda/src/experts.rs:127-250,
+ * kernels/src/lib.rs:3507-3681). */
+uint64_t kh_expert_matmul_workspace(const kh_weight *weight, uint32_t experts, uint64_t k,
+                                    uint64_t tokens, uint32_t topk, uint32_t per_route,
+                                    uint32_t x_kind, uint32_t flags);
+int kh_expert_matmul(const kh_weight *weight, uint32_t experts, uint64_t k, uint32_t x_kind,
+                     const void *x, uint64_t tokens, uint32_t topk, uint32_t per_route,
+                     const uint32_t *idx, uint32_t out_kind, void *out, uint32_t flags,
+                     void *workspace, uint64_t workspace_bytes, void *stream);
 
 /* Host quantization at load time (kapel-core/src/dtype.rs:751-782 for int8,
  * int4, Q8_0, Q4_0, Q4_1, by the reference's rules; Q5_0, Q5_1, Q2_K, Q3_K,

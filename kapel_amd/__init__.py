@@ -87,7 +87,8 @@ _lib = None
 # Every entry point include/kapel_hip.h declares.
 SYMBOLS = ("kh_version", "kh_error_string", "kh_block_len", "kh_block_bytes",
            "kh_qmatmul_workspace", "kh_qmatmul", "kh_quantize_x", "kh_block_dots",
-           "kh_dequantize", "kh_dequantize_rows", "kh_quantize_host")
+           "kh_dequantize", "kh_dequantize_rows", "kh_quantize_host",
+           "kh_expert_matmul_workspace", "kh_expert_matmul")
 
 
 def lib():
@@ -116,6 +117,9 @@ def lib():
     L.kh_dequantize_rows.argtypes = [W, u64, P, u64, u32, P, P]
     L.kh_quantize_host.argtypes = [u32, u32, P, u64, P, ctypes.c_int]
     L.kh_quantize_host.restype = i64
+    L.kh_expert_matmul_workspace.argtypes = [W, u32, u64, u64, u32, u32, u32, u32]
+    L.kh_expert_matmul_workspace.restype = u64
+    L.kh_expert_matmul.argtypes = [W, u32, u64, u32, P, u64, u32, u32, P, u32, P, u32, P, u64, P]
     _lib = L
     return L
 
@@ -251,6 +255,57 @@ class QuantizedMatmul:
         return tuple(x.shape[:-1]) + (n,), x.dtype
 
 
+class IndexOutOfRange(KapelError):
+    pass
+
+
+class ExpertMatmul:
+    """The product of each token by its experts (kapel-ops/src/experts.rs:
+    130-229): x [T, K] or [T, k, K], the experts' weights stacked
+    [E N, K] (one QuantizedTensor), idx [T, k] integers; y [T, k, N] in x's
+    type, y[t, j, n] = sum_i x[t, (j,) i] w[idx[t, j] N + n, i]."""
+
+    NAME = "expert_matmul"
+
+    def __init__(self, experts):
+        self.experts = int(experts)
+
+    def infer(self, inputs):
+        """Shape and type of the output, or the reference's error
+        (kapel-ops/src/experts.rs:166-225)."""
+        if len(inputs) != 3:
+            raise Arity(f"{self.NAME}: expected 3 inputs, got {len(inputs)}")
+        x, w, idx = inputs
+        devices = {str(t.data.device) if isinstance(t, QuantizedTensor) else str(t.device)
+                   for t in inputs}
+        if len(devices) > 1:
+            raise InvalidArgument(f"{self.NAME}: inputs on several devices {sorted(devices)}")
+        float_kind(x.dtype)
+        if idx.dtype.is_floating_point or idx.dim() != 2:
+            raise InvalidArgument(f"{self.NAME}: the experts must be integers [T, k]")
+        if not isinstance(w, QuantizedTensor):
+            raise UnsupportedDType(f"{self.NAME}: weights of type {getattr(w, 'dtype', w)}")
+        t, k = idx.shape
+        width = w.k
+        if tuple(x.shape) not in ((t, width), (t, k, width)):
+            raise InvalidArgument(f"inputs {tuple(x.shape)} for experts {tuple(idx.shape)} and "
+                                  f"weights {w.shape}: [T, K] or [T, k, K]")
+        if self.experts == 0 or w.n % self.experts:
+            raise InvalidArgument(f"{w.n} rows of weights for {self.experts} experts")
+        length = block_len(w.fmt, w.group)
+        if length == 0:
+            raise UnsupportedDType(f"{self.NAME}: format {w.fmt}")
+        if width % length:
+            raise BlockMisaligned(f"{width} elements in blocks of {length}")
+        return (t, k, w.n // self.experts), x.dtype
+
+    def check(self, idx):
+        """experts.rs:151-163: the first index out of range is an error."""
+        bad = [int(i) for i in idx if int(i) >= self.experts or int(i) < 0]
+        if bad:
+            raise IndexOutOfRange(f"{self.NAME}: index {bad[0]} of {self.experts}")
+
+
 class Hip:
     """The HIP backend of the path: one per device ordinal, one stream (the
     current torch stream of that device), a workspace kept between calls."""
@@ -288,8 +343,11 @@ class Hip:
     def stream(self):
         return _torch().cuda.current_stream(self.device).cuda_stream
 
-    def forward(self, op, inputs, out=None, reuse_activations=False):
-        """Run<QuantizedMatmul>::forward: the product on the device."""
+    def forward(self, op, inputs, out=None, reuse_activations=False, check_indices=True):
+        """Run<QuantizedMatmul>::forward (or Run<ExpertMatmul>): the product
+        on the device."""
+        if isinstance(op, ExpertMatmul):
+            return self._experts(op, inputs, out, check_indices)
         if not isinstance(op, QuantizedMatmul):
             raise UnsupportedDType(f"op {op}")
         torch = _torch()
@@ -316,6 +374,36 @@ class Hip:
                                   out.data_ptr() if out.numel() else None, flags, ws.data_ptr(),
                                   ws.numel(), self.stream())
         _raise(status)
+        return out
+
+    def _experts(self, op, inputs, out, check_indices):
+        """kapel-cuda/src/experts.rs:127-250: the indices read (and checked)
+        as the reference's backends do; without the check (check_indices
+        False) an index out of range gives NaN for its route, the device
+        never faults."""
+        torch = _torch()
+        shape, dtype = op.infer(inputs)
+        x, w, idx = inputs
+        if check_indices:
+            op.check(idx.reshape(-1).tolist())
+        x = x.contiguous()
+        if w.data.device != self.device and w.n * w.k > 0:
+            raise InvalidArgument(f"weights on {w.data.device}, backend on {self.device}")
+        tokens, topk = idx.shape
+        per_route = 1 if x.dim() == 3 else 0
+        idx32 = idx.to(self.device, torch.int32).contiguous()
+        if out is None:
+            out = torch.empty(shape, dtype=dtype, device=self.device)
+        weight = w.weight()
+        flags = BYTE_ACTIVATIONS if self.byte_activations else 0
+        size = lib().kh_expert_matmul_workspace(ctypes.byref(weight), op.experts, w.k, tokens, topk,
+                                                per_route, float_kind(x.dtype), flags)
+        ws = self.workspace(size)
+        _raise(lib().kh_expert_matmul(ctypes.byref(weight), op.experts, w.k, float_kind(x.dtype),
+                                      x.data_ptr() if x.numel() else None, tokens, topk, per_route,
+                                      idx32.data_ptr() if idx32.numel() else None, float_kind(dtype),
+                                      out.data_ptr() if out.numel() else None, flags, ws.data_ptr(),
+                                      ws.numel(), self.stream()))
         return out
 
     # -- the pieces, exposed for the parity checks ---------------------------

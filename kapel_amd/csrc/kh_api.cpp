@@ -815,3 +815,139 @@ int kh_dequantize_rows(const kh_weight *weight, uint64_t k, const uint32_t *indi
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- experts
+namespace {
+
+// The shapes of an experts' product (kapel-ops/src/experts.rs:166-225).
+struct Experts {
+    uint64_t n = 0, expert_bytes = 0, routes = 0, xrows = 0, xcopy = 0;
+    int planes = 3;
+    bool mfma = false;
+};
+
+int expert_check(const kh_weight *w, uint32_t experts, uint64_t k, uint64_t tokens, uint32_t topk,
+                 uint32_t per_route, uint32_t x_kind, uint32_t flags, Experts &e) {
+    if (!w) return KH_ERR_NULL;
+    if (!float_kind(x_kind)) return KH_ERR_DTYPE;
+    const uint32_t len = kh_block_len(w->format, w->group), size = kh_block_bytes(w->format, w->group);
+    if (len == 0) return KH_ERR_DTYPE;
+    if (experts == 0 || w->n % experts) return KH_ERR_SHAPE;
+    if (k % len) return KH_ERR_MISALIGNED;
+    if (k > (1ull << 30) || tokens > (1ull << 31) || topk > (1u << 16)) return KH_ERR_OVERFLOW;
+    if (w->bytes != w->n * (k / len) * size) return KH_ERR_SHAPE;
+    if (w->n && k && !w->data) return KH_ERR_NULL;
+    if ((uintptr_t)w->data & 3u) return KH_ERR_SHAPE;
+    e.n = w->n / experts;
+    e.expert_bytes = e.n * (k / len) * size;
+    // Each expert's matrix is read at 32-bit offsets.
+    if (e.expert_bytes >= (1ull << 31)) return KH_ERR_OVERFLOW;
+    e.routes = tokens * topk;
+    if (e.routes > (1ull << 31)) return KH_ERR_OVERFLOW;
+    e.xrows = per_route ? e.routes : tokens;
+    e.xcopy = align_up(e.xrows * k * kind_bytes(x_kind), 256);
+    e.planes = (flags & KH_BYTE_ACTIVATIONS) && byte_format(w->format, w->group) ? 1 : 3;
+    e.mfma = mfma_format(w->format, w->group) && gemv_unit(w->format, w->group) != 0;
+    return KH_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+uint64_t kh_expert_matmul_workspace(const kh_weight *weight, uint32_t experts, uint64_t k,
+                                    uint64_t tokens, uint32_t topk, uint32_t per_route,
+                                    uint32_t x_kind, uint32_t flags) {
+    Experts e;
+    if (expert_check(weight, experts, k, tokens, topk, per_route, x_kind, flags, e) != KH_OK) return 0;
+    return e.xcopy;
+}
+
+int kh_expert_matmul(const kh_weight *weight, uint32_t experts, uint64_t k, uint32_t x_kind,
+                     const void *x, uint64_t tokens, uint32_t topk, uint32_t per_route,
+                     const uint32_t *idx, uint32_t out_kind, void *out, uint32_t flags,
+                     void *workspace, uint64_t workspace_bytes, void *stream) {
+    Experts e;
+    int status = expert_check(weight, experts, k, tokens, topk, per_route, x_kind, flags, e);
+    if (status != KH_OK) return status;
+    if (!float_kind(out_kind)) return KH_ERR_DTYPE;
+    if (e.routes == 0 || e.n == 0) return KH_OK;
+    if (!out || !idx) return KH_ERR_NULL;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (k == 0)
+        return launch_fill_bytes(static_cast<uint8_t *>(out), e.routes * e.n * kind_bytes(out_kind), s) ==
+                       hipSuccess
+                   ? KH_OK
+                   : KH_ERR_HIP;
+    if (!x) return KH_ERR_NULL;
+    // The small-M kernel reads activations by 16 (f32) or 8 bytes.
+    if ((uintptr_t)x % (x_kind == KH_F32 ? 16 : 8)) {
+        if (!workspace || workspace_bytes < e.xcopy || ((uintptr_t)workspace & 255u)) return KH_ERR_WORKSPACE;
+        if (hipMemcpyAsync(workspace, x, e.xrows * k * kind_bytes(x_kind), hipMemcpyDeviceToDevice, s) !=
+            hipSuccess)
+            return KH_ERR_HIP;
+        x = workspace;
+    }
+    const uint32_t len = kh_block_len(weight->format, weight->group);
+    const uint32_t size = kh_block_bytes(weight->format, weight->group);
+    const uint8_t *data = static_cast<const uint8_t *>(weight->data);
+    if (!e.mfma) {
+        GenericArgs g{};
+        g.format = weight->format;
+        g.group = weight->group;
+        g.w = data;
+        g.n = e.n;
+        g.row_bytes = k / len * size;
+        g.k = k;
+        g.rows = e.routes;
+        g.x_kind = x_kind;
+        g.x = x;
+        g.out_kind = out_kind;
+        g.out = out;
+        g.col0 = 0;
+        g.out_stride = e.n;
+        g.experts = idx;
+        g.n_experts = experts;
+        g.topk = (int)topk;
+        g.per_route = per_route ? 1 : 0;
+        g.expert_bytes = e.expert_bytes;
+        return launch_generic(g, s) == hipSuccess ? KH_OK : KH_ERR_HIP;
+    }
+    // One route a chunk of the small-M kernel: its expert's tiles.
+    const int unit = gemv_unit(weight->format, weight->group);
+    const int tiles = (int)div_up(e.n, 16);
+    GemvSplit sp = gemv_split(k, unit, tiles, 1, e.planes, (int)e.routes, false);
+    const uint64_t groups = div_up(div_up(tiles, sp.tiles), 8) * 8;
+    if (groups * e.routes >= (1ull << 31)) return KH_ERR_OVERFLOW;
+    GemvArgs a{};
+    a.count = 1;
+    a.w[0] = data;
+    a.wbytes[0] = (uint32_t)e.expert_bytes;
+    a.n[0] = e.n;
+    a.row_bytes = k / len * size;
+    a.k = (int)k;
+    a.units = sp.units;
+    a.chunk = sp.chunk;
+    a.total_tiles = tiles;
+    a.tiles = sp.tiles;
+    a.tiles_log2 = a.tiles == 4 ? 2 : a.tiles == 2 ? 1 : 0;
+    a.kw = sp.kw;
+    a.rows = 1;
+    a.rows_total = (int)e.routes;
+    a.mchunks = (int)e.routes;
+    a.hi = 65536.0f;
+    a.shift = 8;
+    a.x_kind = x_kind;
+    a.x = x;
+    a.out_kind = out_kind;
+    a.out = out;
+    a.out_stride = e.n;
+    a.width = e.n;
+    a.experts = idx;
+    a.n_experts = experts;
+    a.topk = (int)topk;
+    a.per_route = per_route ? 1 : 0;
+    return launch_gemv(weight->format, weight->group, e.planes, a, s) == hipSuccess ? KH_OK : KH_ERR_HIP;
+}
+
+}  // extern "C"

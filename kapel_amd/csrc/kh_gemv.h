@@ -234,7 +234,12 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     grid_fill<F>();
     const int m0 = mc * a.rows;
     const int rows = min(a.rows, a.rows_total - m0);
-    const XIn xin{static_cast<const uint8_t *>(a.x) + (size_t)m0 * a.k * (XK == X_F32 ? 4 : XK == X_H16 ? 2 : 1),
+    // A route of the experts' product (one row a chunk): its expert and
+    // input row.
+    const uint32_t expert = a.experts ? a.experts[m0] : 0u;
+    const bool bad = a.experts && expert >= a.n_experts;
+    const int64_t xrow = a.experts && !a.per_route ? m0 / a.topk : m0;
+    const XIn xin{static_cast<const uint8_t *>(a.x) + (size_t)xrow * a.k * (XK == X_F32 ? 4 : XK == X_H16 ? 2 : 1),
                   rows, a.k, a.x_kind};
     void *const out = static_cast<uint8_t *>(a.out) + (size_t)m0 * a.out_stride * (a.out_kind == KH_F32 ? 4 : 2);
     int32_t *const dots = a.dots ? a.dots + (size_t)m0 * a.width * (a.k / 16) : nullptr;
@@ -252,8 +257,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         if (ltile >= a.tile0[i] && ltile < a.tile0[i] + (int)((a.n[i] + 15) / 16)) mat = i;
     const int64_t row = (int64_t)(ltile - a.tile0[mat]) * 16 + n16;
     const bool live = any && row < (int64_t)a.n[mat];
-    const lanes::Src src = lanes::source(a.w[mat], a.wbytes[mat]);
-    const uint32_t ro = live ? (uint32_t)row * (uint32_t)a.row_bytes : lanes::NONE;
+    const uint8_t *const wbase = a.experts ? a.w[0] + (size_t)(bad ? 0u : expert) * a.wbytes[0] : a.w[mat];
+    const lanes::Src src = lanes::source(wbase, a.wbytes[mat]);
+    const uint32_t ro = live && !bad ? (uint32_t)row * (uint32_t)a.row_bytes : lanes::NONE;
     const uint64_t col = a.col0[mat] + (uint64_t)row;
     const int blocks32 = a.k / 32;
     auto valid = [&](int u) { return U == 256 || 4 * u + g < blocks32; };
@@ -433,6 +439,9 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         v = v + __shfl_xor(v, 16);
         acc[i] = v + __shfl_xor(v, 32);
     }
+    if (bad)
+#pragma unroll
+        for (int i = 0; i < ACC; i++) acc[i] = __uint_as_float(0x7fc00000u);
     if (a.kw == 1) {
         if (live && g == 0)
 #pragma unroll

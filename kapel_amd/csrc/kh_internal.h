@@ -107,6 +107,13 @@ struct GemvArgs {
     // The kernel with its weights staged in LDS (gemv2_kernel): `npw`
     // preparing waves, `kw` multiplying waves, `tb` copies of 1 KiB a wave.
     int dma, npw, tb;
+    // The experts' product (kh_expert_matmul): a chunk of one activation
+    // row is a route; its weights are expert experts[route] of the stacked
+    // matrix w[0] (wbytes[0] bytes an expert), its input row route (per
+    // route) or route / topk.  An expert of n_experts or more: NaN outputs.
+    const uint32_t *experts;
+    uint32_t n_experts;
+    int topk, per_route;
 };
 
 // The many-row product (kh_mm.h): weights of one format in column groups of
@@ -146,6 +153,12 @@ struct GenericArgs {
     uint32_t out_kind;
     void *out;
     uint64_t col0, out_stride;
+    // The experts' product, as GemvArgs: `rows` routes; n rows an expert
+    // (expert_bytes bytes) of the stacked matrix w.
+    const uint32_t *experts;
+    uint32_t n_experts;
+    int topk, per_route;
+    uint64_t expert_bytes;
 };
 
 struct DequantArgs {

@@ -22,6 +22,7 @@
 //
 // Layouts of the formats: kh_formats.h.  Shapes and refusals: kh_api.cpp.
 #include <hip/hip_fp16.h>
+#include <algorithm>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -539,6 +540,24 @@ __global__ __launch_bounds__(256) void qmv_generic_kernel(GenericArgs a) {
     const int lane = threadIdx.x & 63;
     uint64_t row = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.n) return;
+    if (a.experts) {
+        // The experts' product: route r takes rows of expert experts[r].
+        for (uint64_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
+            const uint32_t e = a.experts[r];
+            const uint64_t xr = a.per_route ? r : r / (uint64_t)a.topk;
+            float acc = 0.0f;
+            if (e < a.n_experts) {
+                const uint8_t *rowp = a.w + e * a.expert_bytes + row * a.row_bytes;
+                for (uint64_t i = lane; i < a.k; i += 64)
+                    acc = fmaf(element(a.format, a.group, rowp, i), load_x(a.x_kind, a.x, xr * a.k + i), acc);
+                for (int s = 32; s >= 1; s >>= 1) acc += __shfl_xor(acc, s);
+            } else {
+                acc = __uint_as_float(0x7fc00000u);
+            }
+            if (lane == 0) store_out(a.out_kind, a.out, r * a.out_stride + row, acc);
+        }
+        return;
+    }
     const uint8_t *rowp = a.w + row * a.row_bytes;
     for (uint64_t m = 0; m < a.rows; m++) {
         float acc = 0.0f;
@@ -629,8 +648,9 @@ hipError_t launch_fill_bytes(uint8_t *p, uint64_t bytes, hipStream_t s) {
 }
 
 hipError_t launch_generic(const GenericArgs &a, hipStream_t s) {
-    if (a.n == 0) return hipSuccess;
-    hipLaunchKernelGGL(qmv_generic_kernel, dim3((unsigned)((a.n + 3) / 4)), dim3(256), 0, s, a);
+    if (a.n == 0 || (a.experts && a.rows == 0)) return hipSuccess;
+    const unsigned routes = a.experts ? (unsigned)std::min<uint64_t>(a.rows, 65535) : 1u;
+    hipLaunchKernelGGL(qmv_generic_kernel, dim3((unsigned)((a.n + 3) / 4), routes), dim3(256), 0, s, a);
     return hipGetLastError();
 }
 

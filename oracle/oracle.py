@@ -179,3 +179,32 @@ def product_bytes(weights, k, x, threads=1, with_dots=False):
                                 rows, _p(out), _p(dots) if with_dots else None, threads)
     assert rc == 0, rc
     return (out, dots) if with_dots else out
+
+
+def expert_product(fmt, group, data, experts, k, x, idx, byte_activations=False, threads=1):
+    """kapel-cpu's experts' product (kapel-cpu/src/experts.rs:62-110): the
+    routes of each expert gathered in route order, multiplied by its rows in
+    one product (the f32 product, or the byte one where the format has it),
+    each result row put back at its route.  ``x`` [T, K] or [T, topk, K],
+    ``idx`` [T, topk] (every index below ``experts``); returns [T, topk, N].
+    """
+    idx = np.asarray(idx).reshape(np.shape(idx)[0], -1)
+    tokens, topk = idx.shape
+    x = np.asarray(x, dtype=np.float32)
+    per_route = x.ndim == 3
+    rows_of = x.reshape(-1, k)
+    data = np.ascontiguousarray(data, dtype=np.uint8)
+    n = data.size // row_bytes(fmt, group, k) // experts if k else 0
+    size = n * row_bytes(fmt, group, k)
+    out = np.zeros((tokens * topk, n), dtype=np.float32)
+    flat = idx.reshape(-1)
+    use_bytes = byte_activations and bytes_supported(fmt, group)
+    for e in range(experts):
+        routes = [r for r in range(tokens * topk) if flat[r] == e]
+        if not routes or n == 0:
+            continue
+        rows = rows_of[[r if per_route else r // topk for r in routes]]
+        w = [(fmt, group, data[e * size:(e + 1) * size], n)]
+        y = product_bytes(w, k, rows, threads) if use_bytes else product_f32(w, k, rows, threads)
+        out[routes] = y
+    return out.reshape(tokens, topk, n)

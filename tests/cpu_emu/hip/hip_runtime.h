@@ -59,6 +59,7 @@ struct Lane {
 };
 inline thread_local Lane self;
 inline dim3 block_dim;
+inline dim3 grid_dim;
 
 struct Block {
     std::barrier<> *all = nullptr;
@@ -280,6 +281,7 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define threadIdx (emu::self.tid)
 #define blockIdx (emu::self.bid)
 #define blockDim (emu::block_dim)
+#define gridDim (emu::grid_dim)
 #define __syncthreads() (emu::block.all->arrive_and_wait())
 #define __threadfence() __atomic_thread_fence(__ATOMIC_SEQ_CST)
 #define __shfl_xor(v, m, ...) emu::shfl_xor((v), (m) __VA_OPT__(, ) __VA_ARGS__)
@@ -409,6 +411,7 @@ void launch(K kernel, dim3 grid, dim3 threads, size_t lds, A... args) {
     if (total == 0) return;
     fresh_block(threads.x, lds);
     block_dim = threads;
+    grid_dim = grid;
     // Between workgroups, the last lane to arrive makes the next one's barriers.
     std::barrier<std::function<void()>> next((ptrdiff_t)threads.x,
                                              std::function<void()>([&] { fresh_block(threads.x, lds); }));

@@ -37,6 +37,7 @@ L.kh_qmatmul.argtypes = [ctypes.POINTER(W), u32, u64, u32, P, u64, u32, P, u32, 
 L.kh_block_dots.argtypes = [ctypes.POINTER(W), u64, P, u64, P, P, u64, P]
 L.kh_quantize_x.argtypes = [u32, P, u64, u64, P, P, P, P]
 L.kh_dequantize.argtypes = [ctypes.POINTER(W), u64, u64, u64, u32, P, P]
+L.kh_expert_matmul.argtypes = [ctypes.POINTER(W), u32, u64, u32, P, u64, u32, u32, P, u32, P, u32, P, u64, P]
 
 HALVES = {Q8_0: [0], Q4_0: [0], Q5_0: [0], Q4_1: [0, 2], Q5_1: [0, 2], Q4K: [0, 2], Q5K: [0, 2],
           Q2K: [80, 82], Q3K: [108], Q6K: [208], IQ4_NL: [0], IQ4_XS: [0], IQ3_S: [0]}
@@ -170,6 +171,32 @@ def case_kinds():
     report("k = 0", bool(np.all(out == 0)))
 
 
+def case_experts(fmt, group, n, k, experts, tokens, topk, per_route, flags=0):
+    """The experts' product against the oracle's (kapel-cpu/src/experts.rs:62-110);
+    an index past the experts gives NaN for its route."""
+    d = blocks(fmt, group, experts * n * k // ko.block_len(fmt, group), 9 + fmt)
+    rng = np.random.default_rng(tokens)
+    idx = rng.integers(0, experts, size=(tokens, topk)).astype(np.uint32)
+    shape = (tokens, topk, k) if per_route else (tokens, k)
+    x = np.ascontiguousarray(rng.uniform(-1, 1, size=shape).astype(np.float32))
+    w = W(fmt, group, d.ctypes.data, d.size, experts * n)
+    bad = idx.copy()
+    bad[0, 0] = experts
+    out = np.zeros((tokens, topk, n), np.float32)
+    st = L.kh_expert_matmul(ctypes.byref(w), experts, k, F32, x.ctypes.data, tokens, topk, int(per_route),
+                            bad.ctypes.data, F32, out.ctypes.data, flags, WORKSPACE.ctypes.data,
+                            WORKSPACE.size, None)
+    assert st == 0, st
+    want = ko.expert_product(fmt, group, d, experts, k, x, idx, byte_activations=bool(flags))
+    name = f"experts fmt {fmt}/{group} n {n} k {k} {tokens}x{topk} of {experts} per_route {per_route} flags {flags}"
+    ok = bool(np.all(np.isnan(out[0, 0])))
+    tol = 1e-4 * (1 + np.abs(want)) if not flags else 2e-4 * (1 + np.abs(want))
+    rest = np.ones((tokens, topk), bool)
+    rest[0, 0] = False
+    ok = ok and bool(np.all(np.abs(out[rest] - want[rest]) <= tol[rest]))
+    report(name, ok)
+
+
 def case_quantize_x():
     x = xs(3, 256, 4)
     x[0, :32] = 0
@@ -232,6 +259,12 @@ def main(which):
     case_product(Q4_0, 0, 20, 96, 33)       # a unit past K (96 = 3 blocks)
     case_product(Q5_1, 0, 20, 160, 9)       # minimums of the 32-element blocks
     case_bytes(INT4, 32, 20, 160, 24, dots=False)
+    # The experts' product: MFMA formats, the generic kernel (int8/40),
+    # inputs per route, byte activations.
+    case_experts(Q8_0, 0, 7, 256, 4, 5, 3, False)
+    case_experts(IQ3_S, 0, 7, 256, 4, 5, 3, True)
+    case_experts(Q4K, 0, 40, 512, 6, 3, 2, False, flags=1)
+    case_experts(INT8, 40, 7, 160, 4, 5, 3, True)
     # The non-linear formats: decode kernels (1, 3 rows), many rows, a unit
     # past K for IQ4_NL.
     case_product(IQ3_S, 0, 40, 512, 3)

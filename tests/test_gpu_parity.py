@@ -391,3 +391,120 @@ def test_qwen3_8b_prefill_at_full_size(hip):
                 col += n
     finally:
         hip.with_byte_activations(False)
+
+
+# ------------------------------------------------------------- experts
+
+EXPERT_FORMATS = [(ka.Q8_0, 0), (ka.IQ4_XS, 0), (ka.IQ3_S, 0), (ka.IQ4_NL, 0), (ka.Q4K, 0),
+                  (ka.Q6K, 0), (ka.INT8, 40)]
+
+
+def expert_f64(fmt, group, data, experts, n, k, x, idx):
+    """kapel-ref/src/experts.rs:64-90: the f64 definition."""
+    size = n * ko.row_bytes(fmt, group, k)
+    dense = {e: ko.dequantize(fmt, group, data[e * size:(e + 1) * size]).reshape(n, k)
+             for e in set(int(v) for v in np.ravel(idx))}
+    tokens, topk = idx.shape
+    rows = x.reshape(tokens, -1, k).astype(np.float64)
+    out = np.zeros((tokens, topk, n))
+    for t in range(tokens):
+        for j in range(topk):
+            out[t, j] = rows[t, j if rows.shape[1] > 1 else 0] @ dense[int(idx[t, j])].T
+    return out
+
+
+@pytest.mark.parametrize("fmt,group", EXPERT_FORMATS)
+def test_expert_products(hip, fmt, group):
+    """conformity.rs:975-990: [5, K] and [5, 3, K] by 3 of 4 experts of
+    [7, K]; within 1e-4 (1 + |e|) of the f64 definition, alongside the
+    CPU's experts' product (kapel-cpu/src/experts.rs:62-110); bitwise the
+    same on a second run."""
+    k = 320 if group == 40 else 256
+    n, experts, tokens, topk = 7, 4, 5, 3
+    data, w = weight(fmt, group, experts * n, k, 40 + fmt, hip)
+    rng = np.random.default_rng(12)
+    idx = rng.integers(0, experts, size=(tokens, topk))
+    op = ka.ExpertMatmul(experts)
+    for per_route in (False, True):
+        shape = (tokens, topk, k) if per_route else (tokens, k)
+        x = rng.uniform(-1, 1, size=shape).astype(np.float32)
+        got = hip.forward(op, [dev(x), w, dev(idx)]).cpu().numpy()
+        assert got.shape == (tokens, topk, n)
+        e64 = expert_f64(fmt, group, data, experts, n, k, x, idx)
+        check_f32(got.reshape(-1, n), e64.reshape(-1, n), f"experts fmt {fmt} per_route {per_route}")
+        cpu = ko.expert_product(fmt, group, data, experts, k, x, idx)
+        assert np.all(np.abs(got - cpu) <= 2e-4 * (1 + np.abs(e64)))
+        again = hip.forward(op, [dev(x), w, dev(idx)]).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_expert_products_in_bf16_and_bytes(hip):
+    """bf16 activations (output bf16), and byte activations for the formats
+    that have them (kapel-cuda/src/experts.rs:166-172 takes bytes for Q8_0):
+    within the bound of bytes.rs:753-770."""
+    k, n, experts, tokens, topk = 512, 24, 6, 4, 2
+    rng = np.random.default_rng(3)
+    idx = rng.integers(0, experts, size=(tokens, topk))
+    op = ka.ExpertMatmul(experts)
+    for fmt in (ka.Q8_0, ka.Q4K):
+        data, w = weight(fmt, 0, experts * n, k, 60 + fmt, hip)
+        x = rng.uniform(-1, 1, size=(tokens, k)).astype(np.float32)
+        xb = torch.from_numpy(x).to(torch.bfloat16)
+        got = hip.forward(op, [xb.to("cuda:0"), w, dev(idx)])
+        assert got.dtype == torch.bfloat16
+        e = expert_f64(fmt, 0, data, experts, n, k, xb.float().numpy(), idx)
+        got = got.float().cpu().numpy()
+        assert np.all(np.abs(got - e) <= 1e-2 * (1 + np.abs(e))), f"bf16 fmt {fmt}"
+        hip.with_byte_activations(True)
+        try:
+            got = hip.forward(op, [dev(x), w, dev(idx)]).cpu().numpy().astype(np.float64)
+        finally:
+            hip.with_byte_activations(False)
+        q, s, _ = ko.quantize_x(x)
+        xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+        dense = ko.dequantize(fmt, 0, data).reshape(experts, n, k)
+        for t in range(tokens):
+            for j in range(topk):
+                d = dense[idx[t, j]]
+                bound = 1e-5 * (np.abs(xq[t]) @ np.abs(d).T) + 1e-6
+                assert np.all(np.abs(got[t, j] - xq[t] @ d.T) <= bound), f"bytes fmt {fmt} {t} {j}"
+
+
+def test_expert_indices_out_of_range(hip):
+    """An index of `experts` or more: the op's check refuses it
+    (experts.rs:151-163); unchecked, its route's outputs are NaN and the
+    others are unchanged (kernels/src/lib.rs:3499-3504)."""
+    k, n, experts = 256, 16, 4
+    data, w = weight(ka.Q4K, 0, experts * n, k, 8, hip)
+    x = np.random.default_rng(1).uniform(-1, 1, size=(2, k)).astype(np.float32)
+    op = ka.ExpertMatmul(experts)
+    idx = np.array([[1, 4], [3, 0]])
+    with pytest.raises(ka.IndexOutOfRange):
+        hip.forward(op, [dev(x), w, dev(idx)])
+    got = hip.forward(op, [dev(x), w, dev(idx)], check_indices=False).cpu().numpy()
+    assert np.all(np.isnan(got[0, 1]))
+    good = np.array([[1, 0], [3, 0]])
+    want = ko.expert_product(ka.Q4K, 0, data, experts, k, x, good)
+    for t, j in ((0, 0), (1, 0), (1, 1)):
+        assert np.all(np.abs(got[t, j] - want[t, j]) <= 2e-4 * (1 + np.abs(want[t, j])))
+
+
+def test_moe_ffn_at_full_size(hip):
+    """A mixture-of-experts FFN at the size of Qwen3-30B-A3B's (128 experts,
+    8 a token, 768 x 2048 gate/up and 2048 x 768 down, Q4_K): decode (1
+    token) and 16 tokens; every route against the CPU's product of its expert
+    for a sample of tokens."""
+    experts, topk, hidden, inner = 128, 8, 2048, 768
+    for name, n, k in (("up", inner, hidden), ("down", hidden, inner)):
+        data, w = weight(ka.Q4K, 0, experts * n, k, 90 + k, hip)
+        for tokens in (1, 16):
+            rng = np.random.default_rng(tokens + k)
+            idx = np.stack([rng.choice(experts, topk, replace=False) for _ in range(tokens)])
+            x = rng.uniform(-1, 1, size=(tokens, k)).astype(np.float32)
+            got = hip.forward(ka.ExpertMatmul(experts), [dev(x), w, dev(idx)]).cpu().numpy()
+            assert np.isfinite(got).all()
+            sample = [0, tokens - 1]
+            want = ko.expert_product(ka.Q4K, 0, data, experts, k, x[sample], idx[sample])
+            e64 = expert_f64(ka.Q4K, 0, data, experts, n, k, x[sample], idx[sample])
+            assert np.all(np.abs(got[sample] - e64) <= 1e-4 * (1 + np.abs(e64))), f"{name} {tokens}"
+            assert np.all(np.abs(got[sample] - want) <= 2e-4 * (1 + np.abs(e64)))

@@ -167,3 +167,51 @@ def test_infer_mirrors_the_reference():
     bad = ka.QuantizedTensor(w.data, ka.Q4K, 0, 5, 200)
     with pytest.raises(ka.BlockMisaligned):
         op.infer([torch.zeros((1, 200)), bad])
+
+
+def expert_call(w, experts, k, tokens, topk, per_route=0, kind=ka.F32, x=8192, idx=8192, out=8192):
+    return ka.lib().kh_expert_matmul(ctypes.byref(w), experts, k, kind, x, tokens, topk, per_route,
+                                     idx, ka.F32, out, 0, None, 0, None)
+
+
+def test_the_experts_abi_refuses_what_infer_refuses():
+    """kapel-ops/src/experts.rs:166-225, as status codes before any device call."""
+    w = weight_struct(ka.Q4K, 0, 4 * 7, 512)
+    assert expert_call(weight_struct(99, 0, 28, 512), 4, 512, 5, 3) == ka.KH_ERR_DTYPE
+    assert expert_call(w, 0, 512, 5, 3) == ka.KH_ERR_SHAPE            # no experts
+    assert expert_call(w, 3, 512, 5, 3) == ka.KH_ERR_SHAPE            # 28 rows for 3
+    assert expert_call(weight_struct(ka.Q4K, 0, 28, 500), 4, 500, 5, 3) == ka.KH_ERR_MISALIGNED
+    assert expert_call(w, 4, 512, 5, 3, kind=9) == ka.KH_ERR_DTYPE
+    assert expert_call(w, 4, 512, 5, 3, idx=None) == ka.KH_ERR_NULL
+    assert expert_call(w, 4, 512, 5, 3, x=None) == ka.KH_ERR_NULL
+    # Misaligned activations need the workspace (none given).
+    assert expert_call(w, 4, 512, 5, 3, x=8196) == ka.KH_ERR_WORKSPACE
+    huge = ka._Weight(ka.Q4K, 0, 4096, (1 << 24) * 144 * 2, 1 << 24)
+    assert expert_call(huge, 1, 512, 1, 1) == ka.KH_ERR_OVERFLOW      # 4.8 GB an expert
+    # Nothing to do.
+    assert expert_call(w, 4, 512, 0, 3) == ka.KH_OK
+    assert expert_call(weight_struct(ka.Q4K, 0, 0, 512), 4, 512, 5, 3) == ka.KH_OK
+    size = ka.lib().kh_expert_matmul_workspace(ctypes.byref(w), 4, 512, 5, 3, 1, ka.F32, 0)
+    assert size >= 5 * 3 * 512 * 4
+    assert ka.lib().kh_expert_matmul_workspace(ctypes.byref(w), 3, 512, 5, 3, 1, ka.F32, 0) == 0
+
+
+def test_expert_infer_mirrors_the_reference():
+    op = ka.ExpertMatmul(4)
+    w = ka.quantized(synth.normal(3, 28 * 256, 0.02).reshape(28, 256), ka.Q8_0)
+    idx = torch.zeros((5, 3), dtype=torch.int64)
+    assert op.infer([torch.zeros((5, 256)), w, idx]) == ((5, 3, 7), torch.float32)
+    assert op.infer([torch.zeros((5, 3, 256), dtype=torch.bfloat16), w, idx]) == ((5, 3, 7), torch.bfloat16)
+    with pytest.raises(ka.Arity):
+        op.infer([torch.zeros((5, 256)), w])
+    with pytest.raises(ka.InvalidArgument):
+        op.infer([torch.zeros((4, 256)), w, idx])
+    with pytest.raises(ka.InvalidArgument):
+        ka.ExpertMatmul(3).infer([torch.zeros((5, 256)), w, idx])
+    with pytest.raises(ka.InvalidArgument):
+        op.infer([torch.zeros((5, 256)), w, idx.float()])
+    with pytest.raises(ka.UnsupportedDType):
+        op.infer([torch.zeros((5, 256)), torch.zeros((28, 256)), idx])
+    with pytest.raises(ka.IndexOutOfRange):
+        op.check([0, 3, 4])
+    op.check([0, 3, 1])

@@ -674,3 +674,50 @@ def test_golden_fixture_matches_the_oracle():
     for case in cases:
         data = np.frombuffer(bytes.fromhex(case["bytes"]), dtype=np.uint8)
         same(ko.dequantize(case["format"], 0, data), case["values"])
+
+
+# ------------------------------------------------------------- experts ---
+
+@pytest.mark.parametrize("fmt", [ko.Q8_0, ko.IQ4_XS, ko.IQ3_S, ko.Q4K])
+@pytest.mark.parametrize("per_route", [False, True])
+def test_expert_product_is_the_reference_definition(fmt, per_route):
+    """conformity.rs:975-990: [5, K] or [5, 3, K] by 3 of 4 experts of
+    [7, 256]; against kapel-ref/src/experts.rs:64-90 (the f64 definition,
+    written here over the dequantized weights), and each route bitwise the
+    f32 product of its own row by its expert alone."""
+    k, n, experts, tokens, topk = 256, 7, 4, 5, 3
+    w = lcg_blocks(fmt, 0, experts * n * k // ko.block_len(fmt), 31)
+    rng = np.random.default_rng(4)
+    idx = rng.integers(0, experts, size=(tokens, topk))
+    shape = (tokens, topk, k) if per_route else (tokens, k)
+    x = rng.uniform(-1, 1, size=shape).astype(np.float32)
+    got = ko.expert_product(fmt, 0, w, experts, k, x, idx)
+    dense = ko.dequantize(fmt, 0, w).reshape(experts, n, k)
+    size = n * ko.row_bytes(fmt, 0, k)
+    for t in range(tokens):
+        for j in range(topk):
+            row = x[t, j] if per_route else x[t]
+            e = row.astype(np.float64) @ dense[idx[t, j]].T
+            assert np.all(np.abs(got[t, j] - e) <= 1e-4 * (1 + np.abs(e))), (t, j)
+            alone = ko.product_f32([(fmt, 0, w[idx[t, j] * size:(idx[t, j] + 1) * size], n)], k,
+                                   row[None])
+            assert np.array_equal(got[t, j].view(np.uint32), alone[0].view(np.uint32)), (t, j)
+
+
+def test_expert_product_in_bytes():
+    """The byte product by experts: within the bound of bytes.rs:753-770 of
+    the exact product of the quantized activations."""
+    k, n, experts = 512, 9, 3
+    w = lcg_blocks(ko.Q4K, 0, experts * n * k // 256, 5)
+    idx = np.array([[2, 0], [1, 2], [2, 2]])
+    x = np.random.default_rng(8).uniform(-1, 1, size=(3, k)).astype(np.float32)
+    got = ko.expert_product(ko.Q4K, 0, w, experts, k, x, idx, byte_activations=True)
+    q, s, _ = ko.quantize_x(x)
+    xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+    dense = ko.dequantize(ko.Q4K, 0, w).reshape(experts, n, k)
+    for t in range(3):
+        for j in range(2):
+            d = dense[idx[t, j]]
+            e = xq[t] @ d.T
+            bound = 1e-5 * (np.abs(xq[t]) @ np.abs(d).T) + 1e-6
+            assert np.all(np.abs(got[t, j] - e) <= bound), (t, j)
