@@ -71,7 +71,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-configs", action="store_true")
-    ap.add_argument("--configs", default="1,3,4,5",
+    ap.add_argument("--configs", default="1,3,4,5,moe",
                     help="which of the other configs to run (comma-separated), after config 2")
     ap.add_argument("--profile", choices=["gateup", "copy"],
                     help="only launch the [gate; up] call (or a 256 MiB device copy) "
@@ -301,6 +301,42 @@ def main():
                             "mfma_frac": round(ops4 / s4 / 1e12 / INT8_PEAK_TOPS, 4),
                             "weight_gbps": round(qbytes / s4 / 1e9, 1)}
             del qlayers
+
+        if "moe" in only:
+            # ---- the experts' product at decode: the shapes of the reference's
+            # kapel-cuda/examples/experts.rs (one token, bf16 x; bytes = the
+            # codes of the experts read).  Weight copies and expert choices
+            # rotate so that no call finds its experts in a cache.
+            cm = {}
+            shapes = [("qwen3.6-35b-a3b", 256, 8, 2048, 512), ("qwen3.8-flash-next", 512, 10, 2560, 640)]
+            for model, experts, topk, hidden, width in shapes:
+                for fmt, what, n, kk in ((ka.IQ3_S, "gate_iq3s", width, hidden),
+                                         (ka.IQ4_XS, "down_iq4xs", hidden, width),
+                                         (ka.Q8_0, "gate_q8_0", width, hidden)):
+                    if kk % ka.block_len(fmt):
+                        continue
+                    rng = np.random.default_rng(experts + n)
+                    size = experts * n * ka.row_bytes(fmt, 0, kk)
+                    raw = rng.integers(0, 256, size=size, dtype=np.uint8)
+                    blocks = raw.reshape(-1, ka.block_bytes(fmt))
+                    blocks[:, 0:2] = np.frombuffer(np.float16(0.01).tobytes(), np.uint8)
+                    copies = max(2, int(1.2e9 // size))
+                    wm = [ka.QuantizedTensor(torch.from_numpy(raw).to(dev), fmt, 0, experts * n, kk)
+                          for _ in range(copies)]
+                    xm = torch.from_numpy(synth.normal(8, kk, 1.0).reshape(1, kk)).to(dev, torch.bfloat16)
+                    om = torch.empty((1, topk, n), device=dev, dtype=torch.bfloat16)
+                    idxs = [torch.tensor([[(c * 101 + i * 37) % experts for i in range(topk)]],
+                                         dtype=torch.int32, device=dev) for c in range(copies)]
+                    mop = ka.ExpertMatmul(experts)
+                    sm, _ = timed([(lambda w=w, ix=ix: hip.forward(mop, [xm, w, ix], out=om, check_indices=False))
+                                   for w, ix in zip(wm, idxs)], 8 * copies, copies)
+                    read = topk * n * ka.row_bytes(fmt, 0, kk)
+                    cm[f"{model}_{what}"] = {"shape": f"1 x {kk} -> {n} x {topk} of {experts}",
+                                             "us": round(sm * 1e6, 2), "gbps": round(read / sm / 1e9, 1)}
+                    del wm
+            configs["moe"] = {"workload": "ExpertMatmul decode (1 token, bf16 x) at the shapes of "
+                                          "kapel-cuda/examples/experts.rs; random codes, f16 scales 0.01",
+                              "calls": cm}
 
     cpu = None
     if not args.no_cpu:
