@@ -242,6 +242,8 @@ def main(which):
     case_product(Q8_0, 0, 5, 96, 2)        # K % 64 == 32: a step of one block
     case_product(Q4K, 0, 100, 2048, 2)      # several tiles and workgroups
     case_product(Q6K, 0, 33, 1024, 3)
+    case_product(Q4K, 0, 40, 4096, 1)       # decode: K split over 4 workgroups
+    case_product(Q6K, 0, 48, 8192, 1)       # decode: K split over 8 workgroups
     case_product(Q4K, 0, 100, 2048, 8)      # K in two chunks of the small-M product
     case_product(Q4_0, 0, 40, 4096, 5)      # four chunks, two waves per tile
     case_product(Q3K, 0, 20, 2048, 7)
