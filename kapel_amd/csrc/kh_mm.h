@@ -749,6 +749,19 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
         float xa[WM], xn[WM], sw;
         v16i dp[P];
         v16f sp;
+        // The unit's activation scales of each row, read whole (16-byte
+        // reads: a read of one scale by the 32 rows of a tile would hit the
+        // same banks four or eight times).
+        float xrow[WM][NS];
+#pragma unroll
+        for (int i = 0; i < WM; i++) {
+            const float4 *q = reinterpret_cast<const float4 *>(sx + (wr + i * 32 + c) * NS);
+#pragma unroll
+            for (int v = 0; v < NS / 4; v++) {
+                const float4 t4 = q[v];
+                xrow[i][4 * v] = t4.x, xrow[i][4 * v + 1] = t4.y, xrow[i][4 * v + 2] = t4.z, xrow[i][4 * v + 3] = t4.w;
+            }
+        }
         // The A operands and activation scales of group j, read a group
         // ahead of their use.
         auto a_operands = [&](int j) __attribute__((always_inline)) {
@@ -762,7 +775,7 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
                 for (int p = 0; p < P; p++)
                     an[i][p] = *reinterpret_cast<const CodeT *>(
                         st + L::OA + (p * RM + r) * AW * 16 + (o ^ L::swz(r)) * 16 + within);
-                xn[i] = h ? 0.0f : sx[r * NS + j * G / 32];
+                xn[i] = h ? 0.0f : xrow[i][j * G / 32];
             }
         };
         a_operands(0);

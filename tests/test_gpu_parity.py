@@ -508,3 +508,25 @@ def test_moe_ffn_at_full_size(hip):
             e64 = expert_f64(ka.Q4K, 0, data, experts, n, k, x[sample], idx[sample])
             assert np.all(np.abs(got[sample] - e64) <= 1e-4 * (1 + np.abs(e64))), f"{name} {tokens}"
             assert np.all(np.abs(got[sample] - want) <= 2e-4 * (1 + np.abs(e64)))
+
+
+def test_gguf_weights_to_the_product(hip, tmp_path):
+    """GGUF on disk to the device (kapel-hub/src/gguf.rs): Q4_K and Q6_K
+    matrices written to a file, mapped, uploaded with their blocks unchanged
+    and multiplied stacked; against the oracle on the file's bytes."""
+    from kapel_amd import gguf
+    k = 1024
+    d1 = random_blocks(ka.Q4K, 0, 40 * k // 256, 81)
+    d2 = random_blocks(ka.Q6K, 0, 24 * k // 256, 82)
+    path = tmp_path / "layer.gguf"
+    gguf.write(path, [("general.architecture", gguf.Entry("string", "llama"))],
+               [("blk.0.ffn_up.weight", ka.QuantizedTensor(torch.from_numpy(d1), ka.Q4K, 0, 40, k)),
+                ("blk.0.ffn_down.weight", ka.QuantizedTensor(torch.from_numpy(d2), ka.Q6K, 0, 24, k))])
+    f = gguf.Gguf.open(path)
+    w1 = f.quantized("blk.0.ffn_up.weight", device="cuda:0")
+    w2 = f.quantized("blk.0.ffn_down.weight", device="cuda:0")
+    x = x_uniform(3, k, 17)
+    got = hip.forward(ka.QuantizedMatmul(), [dev(x), w1, w2]).cpu().numpy()
+    e64 = ko.product_f64([(ka.Q4K, 0, f.raw("blk.0.ffn_up.weight"), 40),
+                          (ka.Q6K, 0, f.raw("blk.0.ffn_down.weight"), 24)], k, x)
+    check_f32(got, e64, "gguf")
