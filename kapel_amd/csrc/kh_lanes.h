@@ -136,16 +136,14 @@ __device__ __forceinline__ v4i hi4(const uint32_t *q) {
 // 2g + 1 of the 6-bit fields (k_scales, quantized.rs:603-616), two lanes of
 // 16 bits each, then each byte to f32.
 __device__ __forceinline__ void k_pair(const uint32_t (&h)[4], int g, float (&s)[2], float (&m)[2]) {
+    // Both forms computed and one selected: lane groups 0-1 and 2-3 of a
+    // wave take different ones, and a branch would run both in turn.
     const int sh = 16 * (g & 1);
-    uint32_t sc, mn;
-    if (g < 2) {
-        sc = (h[1] >> sh) & 0x3f3fu;
-        mn = (h[2] >> sh) & 0x3f3fu;
-    } else {
-        uint32_t lo = h[3] >> sh;
-        sc = (lo & 0x0f0fu) | ((h[1] >> (sh + 2)) & 0x3030u);
-        mn = ((lo >> 4) & 0x0f0fu) | ((h[2] >> (sh + 2)) & 0x3030u);
-    }
+    const uint32_t lo = h[3] >> sh;
+    const uint32_t sc_low = (h[1] >> sh) & 0x3f3fu, mn_low = (h[2] >> sh) & 0x3f3fu;
+    const uint32_t sc_high = (lo & 0x0f0fu) | ((h[1] >> (sh + 2)) & 0x3030u);
+    const uint32_t mn_high = ((lo >> 4) & 0x0f0fu) | ((h[2] >> (sh + 2)) & 0x3030u);
+    const uint32_t sc = g < 2 ? sc_low : sc_high, mn = g < 2 ? mn_low : mn_high;
     const float d = f16(h[0] & 0xffffu), dmin = f16(h[0] >> 16);
     s[0] = d * (float)(sc & 0xffu);
     s[1] = d * (float)(sc >> 8);
