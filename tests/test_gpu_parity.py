@@ -530,3 +530,29 @@ def test_gguf_weights_to_the_product(hip, tmp_path):
     e64 = ko.product_f64([(ka.Q4K, 0, f.raw("blk.0.ffn_up.weight"), 40),
                           (ka.Q6K, 0, f.raw("blk.0.ffn_down.weight"), 24)], k, x)
     check_f32(got, e64, "gguf")
+
+
+def test_unaligned_and_extreme_activations(hip):
+    """Activations that are not 16-byte aligned (copied to the workspace
+    first), rows of zeros, blocks mixing magnitudes 1e-30 to 1e+30, and
+    subnormal values, at M = 1, 3 and 40 (the decode, small-M and many-row
+    kernels): within 1e-4 (1 + |e|) of the f64 product."""
+    k, n = 1024, 40
+    data, w = weight(ka.Q4K, 0, n, k, 33, hip)
+    rng = np.random.default_rng(6)
+    for rows in (1, 3, 40):
+        x = rng.uniform(-1, 1, size=(rows, k)).astype(np.float32)
+        if rows > 1:
+            x[1] = 0.0
+        x[0, 64:96] *= np.float32(1e-30)
+        x[0, 96] = np.float32(1e30) if rows > 1 else np.float32(3.0)
+        x[-1, 128:160] = np.float32(1e-40)
+        base = torch.zeros(rows * k + 1, dtype=torch.float32, device="cuda:0")
+        xt = base[1:].view(rows, k)
+        xt.copy_(dev(x))
+        assert xt.data_ptr() % 16 != 0
+        e64 = ko.product_f64([(ka.Q4K, 0, data, n)], k, x)
+        got = hip.forward(ka.QuantizedMatmul(), [xt, w]).cpu().numpy().astype(np.float64)
+        assert np.all(np.abs(got - e64) <= 1e-4 * (1 + np.abs(e64))), rows
+        if rows > 1:
+            assert np.all(got[1] == 0.0)
