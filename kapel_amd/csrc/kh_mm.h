@@ -24,9 +24,10 @@
 //     of groups, v_mfma_f32_32x32x2_f32 into a sum of the unit's, added to
 //     the sums at the end of the unit.
 //
-// Weights are read straight from HBM by each wave through buffer loads (the
-// lane readers below), one unit ahead; activations are staged per unit in
-// LDS (double-buffered, one barrier per unit) and shared by the four waves.
+// Weights, activation planes, scales and sums of a unit are copied from
+// memory into a ring of two or three LDS stages by direct loads (buffer_load
+// ... lds), the loads of later units in flight while a unit is multiplied
+// (one barrier per unit); the lane readers below read the weights from LDS.
 // Codes are signed where the format's offset is fixed (Q4_0 - 8, Q5_0 - 16,
 // Q6_K - 32, Q3_K - 4, int4 - 8), so those formats have no minimum term.
 //
@@ -554,7 +555,7 @@ constexpr int LDS_MAX = 160 * 1024;      // LDS of a CU (gfx950)
 // instruction writes 64 lanes x 16 bytes, or x 4 bytes, consecutive): the
 // activation rows [P][RM] of the unit's U bytes (16-byte chunks in a
 // swizzled order: chunk o of row r at o ^ swz(r), so that an LDS read of one
-// chunk by 16 rows touches every bank once), the weight rows [NCOLS] of CW
+// chunk by 16 rows touches every bank once), the weight rows [NCOLS] of CWP
 // chunks (the unit's UB bytes from the dword at or below their start), the
 // activation scales [RM][U / 32] and sums [RM][U / G].  Every region is a
 // whole number of instructions for each wave.  A workgroup is WMG x 4 waves:
@@ -566,11 +567,16 @@ struct Plan {
     static constexpr int UB = U / F::BLEN * F::BYTES;
     static constexpr bool ODD = F::BYTES % 4 != 0;  // blocks at even offsets
     static constexpr int CW = (UB + (ODD ? 2 : 0) + 15) / 16;
+    // Chunks a weight row takes in LDS: an odd number (the last one, past
+    // CW, loads nothing), so that the rows read by the 32 lanes of a tile
+    // start 4 banks apart modulo 64 and not on the same few banks (Q6_K's 14
+    // chunks put every fourth row on one bank: 3 % shorter layer at M = 64).
+    static constexpr int CWP = CW | 1;
     static constexpr int AW = U / 16;
     static constexpr int NCOLS = 4 * WN * 32;
     static constexpr int up(int x) { return (x + WAVES - 1) / WAVES * WAVES; }
     static constexpr int IA = up((P * RM * AW + 63) / 64);
-    static constexpr int IW = up((NCOLS * CW + 63) / 64);
+    static constexpr int IW = up((NCOLS * CWP + 63) / 64);
     static constexpr int IS = up((RM * NS + 63) / 64);
     static constexpr int IX = F::MIN ? up((RM * NX + 63) / 64) : 0;
     static constexpr int OA = 0, OW = IA * 1024, OS = OW + IW * 1024, OX = OS + IS * 256;
@@ -625,7 +631,7 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
     using L = Plan<F, P, WM, WMG, WN>;
     constexpr int WAVES = L::WAVES;
     constexpr int U = F::U, G = F::G, NG = F::NG, RM = L::RM, NS = L::NS, NX = L::NX;
-    constexpr int S = L::STAGES, AW = L::AW, CW = L::CW;
+    constexpr int S = L::STAGES, AW = L::AW, CW = L::CW, CWP = L::CWP;
     using CodeT = decltype(F::codes(*(const typename F::Regs *)nullptr, 0, 0));
     extern __shared__ __align__(16) uint8_t lds[];
 
@@ -670,10 +676,10 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < DW; i++) {
-        const int ci = (i * WAVES + wave) * 64 + lane, col = ci / CW;
+        const int ci = (i * WAVES + wave) * 64 + lane, col = ci / CWP;
         const int64_t n = g0 + col;
-        w_row[i] = ci < L::NCOLS * CW && n < nmat ? (uint32_t)n * row_bytes : NONE;
-        w_piece[i] = 16 * (ci % CW);
+        w_row[i] = ci < L::NCOLS * CWP && ci % CWP < CW && n < nmat ? (uint32_t)n * row_bytes : NONE;
+        w_piece[i] = 16 * (ci % CWP);
     }
 #pragma unroll
     for (int i = 0; i < DS; i++) {
@@ -736,7 +742,7 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
         for (int t = 0; t < WN; t++) {
             const int col = wc + t * 32 + c;
             const uint32_t shift = L::ODD ? (((uint32_t)(g0 + col) * row_bytes + (uint32_t)u * L::UB) & 3u) : 0u;
-            F::load(R[t], Lds{st + L::OW}, (uint32_t)(col * CW * 16) + shift, 0, h);
+            F::load(R[t], Lds{st + L::OW}, (uint32_t)(col * CWP * 16) + shift, 0, h);
         }
         // The steps (group j, weight tile t, row tile i) in order, as a
         // pipeline: the MFMAs of a step are issued before the VALU work of
