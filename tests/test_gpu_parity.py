@@ -556,3 +556,46 @@ def test_unaligned_and_extreme_activations(hip):
         assert np.all(np.abs(got - e64) <= 1e-4 * (1 + np.abs(e64))), rows
         if rows > 1:
             assert np.all(got[1] == 0.0)
+
+
+def test_outputs_written_in_full_and_workspace_reused(hip):
+    """kapel-cuda/src/lib.rs:70-74 (outputs poisoned before each op: a part
+    left unwritten gives NaN): every kernel path writes its whole output.
+    Launches of different shapes, kinds and formats share one workspace and
+    run interleaved, twice, on the default and on another stream: every
+    result is bitwise the same (the workspace's counters return to their
+    starting state after each launch; nothing depends on the stream)."""
+    k = 1280
+    mats = {}
+    for i, (fmt, group) in enumerate([(ka.Q4K, 0), (ka.Q6K, 0), (ka.Q8_0, 0), (ka.Q4_0, 0), (ka.INT4, 32)]):
+        mats[fmt] = [weight(fmt, group, n, k, 300 + 10 * i + j, hip) for j, n in enumerate((48, 16))]
+    cases = [(fmt, rows, byte) for fmt in mats for rows in (1, 3, 17, 64) for byte in (False, True)]
+    xs = {rows: dev(x_uniform(rows, k, 400 + rows)) for rows in (1, 3, 17, 64)}
+
+    def run(fmt, rows, byte):
+        hip.with_byte_activations(byte)
+        ws = [w for _, w in mats[fmt]]
+        out = torch.full((rows, sum(w.n for w in ws)), float("nan"), device="cuda:0")
+        hip.forward(ka.QuantizedMatmul(), [xs[rows]] + ws, out=out)
+        return out
+
+    try:
+        first = {}
+        for case in cases:
+            out = run(*case).cpu().numpy()
+            assert not np.isnan(out).any(), f"unwritten outputs: format {case[0]}, rows {case[1]}, bytes {case[2]}"
+            first[case] = out
+            if case[1] == 3 and not case[2]:
+                data = [(case[0], w.group, d, w.n) for d, w in mats[case[0]]]
+                check_f32(out, ko.product_f64(data, k, xs[3].cpu().numpy()), f"format {case[0]} stacked")
+        side = torch.cuda.Stream()
+        for use_side in (False, True):
+            with torch.cuda.stream(side if use_side else torch.cuda.current_stream()):
+                again = {case: run(*case) for case in reversed(cases)}
+            torch.cuda.synchronize()
+            for case in cases:
+                got = again[case].cpu().numpy()
+                assert np.array_equal(got.view(np.uint32), first[case].view(np.uint32)), \
+                    f"format {case[0]}, rows {case[1]}, bytes {case[2]}, side stream {use_side}"
+    finally:
+        hip.with_byte_activations(False)
