@@ -551,6 +551,7 @@ struct IQ3S {
 // ---------------------------------------------------------- the kernel
 constexpr int LDS_MAX = 160 * 1024;      // LDS of a CU (gfx950)
 
+
 // The LDS stage of one unit, filled by direct loads to LDS (each wave
 // instruction writes 64 lanes x 16 bytes, or x 4 bytes, consecutive): the
 // activation rows [P][RM] of the unit's U bytes (16-byte chunks in a
@@ -888,7 +889,47 @@ __global__ __launch_bounds__(256 * WMG) void mm_kernel(MmArgs a) {
     wait_vm<0>();
 
     // Lane (c, h), register v of a tile holds row 8 (v / 4) + 4h + v % 4,
-    // column c.
+    // column c.  The workgroup's sums go through LDS ([RM][NCOLS + 8]
+    // floats: the two halves of a wave 32 banks apart), then out as 16-byte
+    // stores of 4 consecutive columns: whole rows of 512 or 1024 bytes
+    // instead of two 128-byte pieces an instruction (config 4's layer 2-3 %
+    // shorter).
+    constexpr int TS = L::NCOLS + 8;
+    if constexpr (RM * TS * 4 <= S * L::SB) {
+        float *tile = reinterpret_cast<float *>(lds);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int t = 0; t < WN; t++)
+#pragma unroll
+                for (int v = 0; v < 16; v++)
+                    tile[(wr + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3)) * TS + wc + t * 32 + c] = acc[i][t][v];
+        __syncthreads();
+        const bool partial = a.ks > 1;
+        float *dst = partial ? a.partials + (uint64_t)kz * a.rows * a.width : static_cast<float *>(a.out);
+        const uint64_t stride = partial ? a.width : a.out_stride;
+        const bool f32 = partial || a.out_kind == KH_F32;
+        const bool vec = f32 && (((uintptr_t)dst & 15u) == 0) && stride % 4 == 0 && a.col0[mat] % 4 == 0;
+        for (int idx = threadIdx.x; idx < RM * (L::NCOLS / 4); idx += 64 * WAVES) {
+            const int r = idx / (L::NCOLS / 4), c4 = 4 * (idx % (L::NCOLS / 4));
+            const int m = m0 + r;
+            const int64_t n = g0 + c4;
+            if (m >= a.rows || n >= nmat) continue;
+            const float4 y = *reinterpret_cast<const float4 *>(tile + r * TS + c4);
+            const uint64_t at = (uint64_t)m * stride + a.col0[mat] + (uint64_t)n;
+            if (vec && n + 4 <= nmat) {
+                *reinterpret_cast<float4 *>(dst + at) = y;
+            } else {
+                const float ys[4] = {y.x, y.y, y.z, y.w};
+                for (int e = 0; e < 4 && n + e < nmat; e++) {
+                    if (f32) dst[at + e] = ys[e];
+                    else store_out(a.out_kind, a.out, at + e, ys[e]);
+                }
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < WM; i++)
 #pragma unroll
