@@ -201,7 +201,7 @@ Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     // would leave 10 of them idle half the time; measured: Q2_K 12288 x 4096
     // at M = 1 30 % shorter, Q3_K 21 %, Q4_0 8192 x 2048 5 %).
     int most = std::min(16 - p.npw, units);
-    most = (int)div_up(units, div_up(units, most));
+    if (most > 0) most = (int)div_up(units, div_up(units, most));
     for (int t = tiles; t >= 1; t /= 2)
         for (int kw = most; kw >= 1; kw--) {
             const int upw = (int)div_up(units, kw);
