@@ -74,12 +74,19 @@ extern "C" {
 /* Flags of kh_qmatmul. */
 /* Activations quantized to bytes by blocks of 32 (kapel-cpu/src/bytes.rs),
  * integer block dots; taken only if every weight's format is read that way
- * (bytes.rs:51-77), as Cpu::with_byte_activations (matmul.rs:293). */
+ * (bytes.rs:51-77) and x has at most 16 rows, as Cpu::with_byte_activations
+ * (kapel-cpu/src/matmul.rs:14,292-306: above IN_PLACE_ROWS = 16 rows the CPU
+ * multiplies dequantized f32 tiles, and so does this library). */
 #define KH_BYTE_ACTIVATIONS 1u
 /* The activations were prepared in this workspace by the previous call with
  * the same x, rows, k and mode: the call goes straight to the products (for
  * one x multiplied by weights given in several calls). */
 #define KH_REUSE_ACTIVATIONS 2u
+/* Byte activations at every row count (batched decode and prefill in
+ * bytes, the int8 MFMA product): as KH_BYTE_ACTIVATIONS without its 16-row
+ * limit.  A divergence from kapel-cpu, whose products above 16 rows are f32
+ * whatever the mode; it has no counterpart in the reference. */
+#define KH_BYTE_ACTIVATIONS_ALL_ROWS 4u
 
 /* One weight matrix of a product: n rows of k elements, `bytes` bytes of
  * blocks at `data` (device), the rows stacked after those of the previous

@@ -33,6 +33,7 @@ FORMAT_NAMES = {INT8: "int8", INT4: "int4", Q8_0: "q8_0", Q4_0: "q4_0", Q4_1: "q
 # Float types (kapel-cuda-abi/src/lib.rs:152-163).
 F32, BF16, F16 = 0, 1, 2
 BYTE_ACTIVATIONS = 1
+BYTE_ACTIVATIONS_ALL_ROWS = 4
 REUSE_ACTIVATIONS = 2
 
 KH_OK, KH_ERR_ARITY, KH_ERR_DTYPE, KH_ERR_SHAPE, KH_ERR_MISALIGNED = 0, 1, 2, 3, 4
@@ -316,14 +317,24 @@ class Hip:
             raise DeviceError("no HIP device")
         self.device = torch.device("cuda", ordinal)
         self.byte_activations = False
+        self.byte_rows_all = False
         self._workspace = None
         lib()
 
-    def with_byte_activations(self, on=True):
+    def with_byte_activations(self, on=True, all_rows=False):
         """kapel-cpu/src/backend.rs:71-81: activations quantized to bytes by
-        blocks of 32 in the products by quantized weights."""
+        blocks of 32 in the products by quantized weights, for x of up to 16
+        rows as kapel-cpu/src/matmul.rs:292-306 (more rows: f32).  all_rows:
+        bytes at every row count (KH_BYTE_ACTIVATIONS_ALL_ROWS, the int8 MFMA
+        product of batched decode and prefill; not a mode of the reference)."""
         self.byte_activations = bool(on)
+        self.byte_rows_all = bool(on) and bool(all_rows)
         return self
+
+    def _flags(self):
+        if self.byte_rows_all:
+            return BYTE_ACTIVATIONS_ALL_ROWS
+        return BYTE_ACTIVATIONS if self.byte_activations else 0
 
     def upload(self, t):
         if isinstance(t, QuantizedTensor):
@@ -364,7 +375,7 @@ class Hip:
         if out is None:
             out = torch.empty(shape, dtype=dtype, device=self.device)
         array = (_Weight * len(weights))(*[w.weight() for w in weights])
-        flags = BYTE_ACTIVATIONS if self.byte_activations else 0
+        flags = self._flags()
         size = lib().kh_qmatmul_workspace(array, len(weights), k, rows, flags)
         if reuse_activations:
             flags |= REUSE_ACTIVATIONS

@@ -218,6 +218,14 @@ Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     return p;
 }
 
+// The small-M kernel's bounded wait for its activations: 2^24 spins, or
+// KH_SPIN_LIMIT from the environment (a test hook: negative gives up at once,
+// which must leave NaN outputs, never wrong numbers).
+int spin_limit() {
+    const char *e = getenv("KH_SPIN_LIMIT");
+    return e ? atoi(e) : 1 << 24;
+}
+
 // The workspace: the counters of the segment split (fixed, first), the
 // prepared activations, then the partial sums.
 struct Layout {
@@ -374,7 +382,10 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
         tiles += div_up(w.n, 16);
     }
     if (c.width > (1ull << 31)) return KH_ERR_OVERFLOW;
-    c.bytes = (flags & KH_BYTE_ACTIVATIONS) && all_bytes;
+    // kapel-cpu/src/matmul.rs:292-306: bytes only in place, up to 16 rows
+    // (IN_PLACE_ROWS), unless the caller asks for them at every row count.
+    const bool byte_rows = (flags & KH_BYTE_ACTIVATIONS_ALL_ROWS) || ((flags & KH_BYTE_ACTIVATIONS) && rows <= 16);
+    c.bytes = byte_rows && all_bytes;
     c.max_wgs = div_up(tiles, 4) + count;
     if (c.max_wgs > MAX_COUNTERS) return KH_ERR_OVERFLOW;
     if (k > 0 && rows > 0)
@@ -451,6 +462,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
         const kh_weight &w = weights[L.members[0]];
         if (L.gemv) {
             GemvArgs a{};
+            a.spin_limit = spin_limit();
             a.count = (int)L.members.size();
             int tiles = 0;
             for (int m = 0; m < a.count; m++) {
@@ -699,7 +711,7 @@ int kh_quantize_x(uint32_t x_kind, const void *x, uint64_t rows, uint64_t k, int
 int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t rows,
                   int32_t *dots, void *workspace, uint64_t workspace_bytes, void *stream) {
     Checked c;
-    int status = check(weight, 1, k, rows, KH_BYTE_ACTIVATIONS, c);
+    int status = check(weight, 1, k, rows, KH_BYTE_ACTIVATIONS_ALL_ROWS, c);
     if (status != KH_OK) return status;
     if (!c.bytes) return KH_ERR_DTYPE;
     if (rows == 0 || weight->n == 0 || k == 0) return KH_OK;
@@ -725,6 +737,7 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     if (unit && rows <= GEMV_ROWS && (uintptr_t)q % 4 == 0 && w.bytes < (1ull << 31)) {
         // The bytes go through the small-M product's own preparation.
         GemvArgs g{};
+        g.spin_limit = spin_limit();
         g.count = 1;
         g.w[0] = static_cast<const uint8_t *>(w.data);
         g.wbytes[0] = (uint32_t)w.bytes;
@@ -929,6 +942,7 @@ int kh_expert_matmul(const kh_weight *weight, uint32_t experts, uint64_t k, uint
     const uint64_t groups = div_up(div_up(tiles, sp.tiles), 8) * 8;
     if (groups * e.routes >= (1ull << 31)) return KH_ERR_OVERFLOW;
     GemvArgs a{};
+    a.spin_limit = spin_limit();
     a.count = 1;
     a.w[0] = data;
     a.wbytes[0] = (uint32_t)e.expert_bytes;

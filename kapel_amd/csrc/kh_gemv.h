@@ -371,6 +371,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
     const int qpc = rows * span / 4;  // quads of a chunk
     const int npw = min((int)(blockDim.x >> 6), (qpc + 64 * PASSES - 1) / (64 * PASSES));
     const bool prep = wave < npw;
+    bool stalled = false;
     int *ready = reinterpret_cast<int *>(lds);
     if (threadIdx.x == 0) *ready = 0;
     __syncthreads();
@@ -414,11 +415,16 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         }
 #pragma unroll
         for (int j = 0; j < NB; j++) load(R[j], c0 + kw + j * step, c1);
-        // Bounded: a wait that never ended would hang the device.
-        for (int spin = 0; spin < (1 << 24); spin++) {
+        // Bounded: a wait that never ended would hang the device.  A wait
+        // that gives up leaves the workgroup's outputs NaN (never silently
+        // wrong numbers).
+        for (int spin = 0; spin < a.spin_limit; spin++) {
             if (__hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= npw * ci) break;
             __builtin_amdgcn_s_sleep(1);
         }
+        if (a.spin_limit < 0 ||
+            __hip_atomic_load(ready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < npw * ci)
+            stalled = true;
         for (int base = c0 + kw; base < c1; base += NB * step) {
 #pragma unroll
             for (int j = 0; j < NB; j++) {
@@ -439,7 +445,7 @@ __global__ __launch_bounds__(64 * W) void gemv_kernel(GemvArgs a) {
         v = v + __shfl_xor(v, 16);
         acc[i] = v + __shfl_xor(v, 32);
     }
-    if (bad)
+    if (bad || stalled)
 #pragma unroll
         for (int i = 0; i < ACC; i++) acc[i] = __uint_as_float(0x7fc00000u);
     if (a.kw == 1) {
@@ -749,14 +755,10 @@ namespace {
 
 template <class F, int P, int MT, int XK>
 hipError_t launch2(const GemvArgs &a, hipStream_t s, size_t lds) {
-    static bool ready = false;
-    if (!ready) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv2_kernel<F, P, MT, XK>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize,
-                                           160 * 1024 - grid_lds<F>());
-        if (e != hipSuccess) return e;
-        ready = true;
-    }
+    static OncePerDevice once;
+    hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&gemv2_kernel<F, P, MT, XK>),
+                                 160 * 1024 - grid_lds<F>());
+    if (e != hipSuccess) return e;
     const int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
     hipLaunchKernelGGL((gemv2_kernel<F, P, MT, XK>), dim3((unsigned)groups), dim3(64 * (a.npw + a.kw)), lds, s, a);
     return hipGetLastError();

@@ -3,6 +3,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/kapel_hip.h"
 
 namespace kh {
@@ -28,6 +30,26 @@ constexpr int MAX_SEGS = 64;
 constexpr uint64_t MAX_COUNTERS = 1u << 16;
 // LDS of one workgroup of the product at most.
 constexpr int MAX_LDS = 64 * 1024;
+
+// A kernel's dynamic LDS limit, raised once per device: std::call_once per
+// device ordinal, so that host threads making their first calls at once do
+// not race (the attribute is per device).
+constexpr int MAX_DEVICES = 64;
+struct OncePerDevice {
+    std::once_flag flag[MAX_DEVICES];
+    hipError_t err[MAX_DEVICES] = {};
+};
+
+inline hipError_t set_lds_limit(OncePerDevice &once, const void *kernel, int bytes) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    std::call_once(once.flag[dev], [&] {
+        once.err[dev] = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    });
+    return once.err[dev];
+}
 
 struct PrepArgs {
     uint32_t x_kind;
@@ -114,6 +136,10 @@ struct GemvArgs {
     const uint32_t *experts;
     uint32_t n_experts;
     int topk, per_route;
+    // Spins of a wave waiting for the activations in LDS before it gives up
+    // (its outputs then NaN): 2^24; negative (a test of the path only):
+    // give up at once.
+    int spin_limit;
 };
 
 // The many-row product (kh_mm.h): weights of one format in column groups of

@@ -956,13 +956,9 @@ hipError_t launch_w(const MmArgs &a, hipStream_t s) {
     using L = Plan<F, P, WM, WMG, wn_of<F, P, WM, WMG>()>;
     static_assert(L::FITS, "two stages fit in LDS");
     constexpr size_t bytes = (size_t)L::STAGES * L::SB;
-    static bool ready = false;
-    if (!ready) {
-        hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void *>(&mm_kernel<F, P, WM, WMG>),
-                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-        if (e != hipSuccess) return e;
-        ready = true;
-    }
+    static OncePerDevice once;
+    hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&mm_kernel<F, P, WM, WMG>), (int)bytes);
+    if (e != hipSuccess) return e;
     const int groups = a.ngroups * a.ks;
     dim3 grid((unsigned)((groups + XCDS - 1) / XCDS * XCDS * a.mtiles)), block(64 * L::WAVES);
     hipLaunchKernelGGL((mm_kernel<F, P, WM, WMG>), grid, block, bytes, s, a);

@@ -35,7 +35,7 @@ struct dim3 {
     constexpr dim3(unsigned a = 1, unsigned b = 1, unsigned c = 1) : x(a), y(b), z(c) {}
 };
 typedef int hipError_t;
-enum { hipSuccess = 0, hipErrorInvalidValue = 1 };
+enum { hipSuccess = 0, hipErrorInvalidValue = 1, hipErrorInvalidDevice = 101 };
 typedef struct ihipStream_t *hipStream_t;
 struct int2 {
     int x, y;
@@ -317,6 +317,10 @@ typedef emu::BufferRsrc __amdgpu_buffer_rsrc_t;
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
 enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
+inline hipError_t hipGetDevice(int *dev) {
+    *dev = 0;
+    return hipSuccess;
+}
 inline hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int bytes) {
     return bytes <= (int)emu::LDS_BYTES ? hipSuccess : hipErrorInvalidValue;
 }

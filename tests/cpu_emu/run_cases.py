@@ -126,19 +126,36 @@ def case_bytes(fmt, group, n, k, rows, dots=True):
     out_cpu, dots_cpu = ko.product_bytes([(fmt, group, d, n)], k, x, with_dots=True)
     q, s, _ = ko.quantize_x(x)
     w = W(fmt, group, d.ctypes.data, d.size, n)
-    size = L.kh_qmatmul_workspace(ctypes.byref(w), 1, k, rows, 1)
+    flags = 1 if rows <= 16 else 4  # bytes above 16 rows: KH_BYTE_ACTIVATIONS_ALL_ROWS
+    size = L.kh_qmatmul_workspace(ctypes.byref(w), 1, k, rows, flags)
     ws = workspace(size)
     if dots:
         dots = np.zeros((rows, n, k // 16), np.int32)
         assert L.kh_block_dots(ctypes.byref(w), k, q.ctypes.data, rows, dots.ctypes.data,
                                ws.ctypes.data, ws.size, None) == 0
         report(f"dots fmt {fmt}/{group} rows {rows}", bool(np.array_equal(dots, dots_cpu)))
-    got = product([(fmt, group, d, n)], k, x, flags=1).astype(np.float64)
+    got = product([(fmt, group, d, n)], k, x, flags=flags).astype(np.float64)
     dense = ko.dequantize(fmt, group, d).reshape(n, k)
     xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
     e = xq @ dense.T
     size = np.abs(xq) @ np.abs(dense).T
     report(f"bytes fmt {fmt}/{group} rows {rows}", bool(np.all(np.abs(got - e) <= 1e-5 * size + 1e-6)))
+
+
+def case_stalled_wait():
+    """The small-M kernel's bounded wait for its activations, forced to
+    give up (KH_SPIN_LIMIT negative): every output NaN, none wrong; then the
+    normal wait again gives the product."""
+    d = blocks(Q4K, 0, 20 * 1024 // 256, 9)
+    x = xs(3, 1024, 4)
+    os.environ["KH_SPIN_LIMIT"] = "-1"
+    try:
+        got = product([(Q4K, 0, d, 20)], 1024, x)
+    finally:
+        del os.environ["KH_SPIN_LIMIT"]
+    report("stalled wait: NaN outputs", bool(np.isnan(got).all()))
+    check_f32("after a stalled wait", product([(Q4K, 0, d, 20)], 1024, x),
+              ko.product_f64([(Q4K, 0, d, 20)], 1024, x))
 
 
 def case_kinds():
@@ -236,6 +253,7 @@ def main(which):
     case_product(INT8, 64, 7, 1280, 1)
     case_quantize_x()
     case_kinds()
+    case_stalled_wait()
     for fmt, group in FORMATS:
         case_product(fmt, group, 7, 1280, 1)
         case_dequantize(fmt, group)

@@ -184,7 +184,7 @@ def test_byte_products_and_block_dots(hip, fmt, group):
         q, s, _ = ko.quantize_x(x)
         dots = hip.block_dots(w, dev(q)).cpu().numpy()
         assert np.array_equal(dots, dots_cpu), f"fmt {fmt} rows {rows}"
-        got = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w])
+        got = hip.with_byte_activations(True, all_rows=rows > 16).forward(ka.QuantizedMatmul(), [dev(x), w])
         hip.with_byte_activations(False)
         got = got.cpu().numpy().astype(np.float64)
         dense = ko.dequantize(fmt, group, data).reshape(n, k)
@@ -193,6 +193,49 @@ def test_byte_products_and_block_dots(hip, fmt, group):
         size = np.abs(xq) @ np.abs(dense).T
         assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6), f"fmt {fmt} rows {rows}"
         assert np.all(np.abs(got - out_cpu) <= 2e-5 * size + 2e-6)
+
+
+def test_byte_mode_stops_at_sixteen_rows(hip):
+    """kapel-cpu/src/matmul.rs:14,292-306: byte activations only for x of at
+    most 16 rows (IN_PLACE_ROWS); above, the product is the f32 one, bit for
+    bit, unless bytes are asked for at every row count
+    (KH_BYTE_ACTIVATIONS_ALL_ROWS, then within the byte bound)."""
+    k, n = 1024, 40
+    data, w = weight(ka.Q4K, 0, n, k, 77, hip)
+    for rows in (16, 17, 64):
+        x = x_uniform(rows, k, 500 + rows)
+        f32 = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        byte = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        every = hip.with_byte_activations(True, all_rows=True).forward(ka.QuantizedMatmul(), [dev(x), w])
+        hip.with_byte_activations(False)
+        e, size = exact_bytes(ka.Q4K, 0, data, n, k, x)
+        assert np.all(np.abs(every.cpu().numpy().astype(np.float64) - e) <= 1e-5 * size + 1e-6), rows
+        if rows <= 16:
+            assert np.all(np.abs(byte.astype(np.float64) - e) <= 1e-5 * size + 1e-6), rows
+            assert not np.array_equal(byte, f32)
+        else:
+            assert np.array_equal(byte.view(np.uint32), f32.view(np.uint32)), rows
+
+
+def test_reused_activations(hip):
+    """KH_REUSE_ACTIVATIONS: one x by weights given in several calls, the
+    activations prepared by the first call only (the many-row product's
+    prepared planes): bitwise equal to the calls without reuse, f32 and
+    bytes."""
+    k = 1280
+    hip.workspace(64 << 20)  # one workspace for all the calls
+    parts = [weight(ka.Q4K, 0, 300, k, 90, hip), weight(ka.Q4K, 0, 200, k, 91, hip)]
+    x = dev(x_uniform(40, k, 7))
+    for byte in (False, True):
+        hip.with_byte_activations(byte, all_rows=byte)
+        try:
+            plain = [hip.forward(ka.QuantizedMatmul(), [x, w]).cpu().numpy() for _, w in parts]
+            first = hip.forward(ka.QuantizedMatmul(), [x, parts[0][1]]).cpu().numpy()
+            second = hip.forward(ka.QuantizedMatmul(), [x, parts[1][1]], reuse_activations=True).cpu().numpy()
+        finally:
+            hip.with_byte_activations(False)
+        assert np.array_equal(first.view(np.uint32), plain[0].view(np.uint32))
+        assert np.array_equal(second.view(np.uint32), plain[1].view(np.uint32)), byte
 
 
 def test_byte_mode_falls_back_for_other_formats(hip):
@@ -257,7 +300,7 @@ def test_llama_3b_layer_at_full_size(hip, byte):
     each matrix is checked against the oracle; every output is finite and a
     second run is bitwise equal."""
     rows = 64 if byte else 1
-    hip.with_byte_activations(byte)
+    hip.with_byte_activations(byte, all_rows=byte)
     try:
         mats = {name: synth_weight(fmt, 0, n, k, 1000 + i) + (fmt, n, k)
                 for i, (name, n, k, fmt) in enumerate(LLAMA_3B)}
@@ -275,27 +318,97 @@ def test_llama_3b_layer_at_full_size(hip, byte):
                 sample = np.linspace(0, n - 1, 96).astype(int)
                 rb = ko.row_bytes(fmt, 0, kk)
                 sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
-                xr = x[: min(rows, 8)]
+                # Rows from every 32-row tile of the launch: 0-3, 31, 32,
+                # 47, 60-63 at M = 64.
+                pick = np.unique(np.r_[0:4, 31, 32, 47, rows - 4:rows]) if byte else np.r_[0:1]
+                xr = x[pick]
                 if byte:
                     want = ko.product_bytes([(fmt, 0, sub, len(sample))], kk, xr)
                     q, s, _ = ko.quantize_x(xr)
                     dense = ko.dequantize(fmt, 0, sub).reshape(len(sample), kk)
                     xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
                     size = np.abs(xq) @ np.abs(dense).T
-                    assert np.all(np.abs(got[: len(xr), col + sample] - want) <= 2e-5 * size + 2e-6), c
+                    assert np.all(np.abs(got[pick][:, col + sample] - want) <= 2e-5 * size + 2e-6), c
                 else:
                     e64 = ko.product_f64([(fmt, 0, sub, len(sample))], kk, xr)
-                    check_f32(got[: len(xr), col + sample], e64, c)
+                    check_f32(got[pick][:, col + sample], e64, c)
                 col += n
     finally:
         hip.with_byte_activations(False)
 
 
+def test_config_1_exactly(hip):
+    """Config 1: Q4_0 8192 x 2048 from N(0, 0.02) values of seed 0, x from
+    N(0, 1) of seed 1; all 8192 outputs against the f64 product within
+    1e-4 max(1, max|y|) (kapel-ref/src/conformity.rs:1835-1840) and 1e-4 (1 +
+    |e|), and a second run bitwise equal."""
+    n, k = 8192, 2048
+    data = ka.quantize(ka.Q4_0, 0, synth.normal(0, n * k, 0.02))
+    w = ka.QuantizedTensor(dev(data), ka.Q4_0, 0, n, k)
+    x = synth.normal(1, k, 1.0).reshape(1, k)
+    got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+    again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+    e64 = ko.product_f64([(ka.Q4_0, 0, data, n)], k, x)
+    check_f32(got, e64, "config 1")
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_config_5_output_table_at_full_size(hip):
+    """Config 5's Q6_K output table, 151936 x 4096 (510 MB), at M = 1 and 8:
+    every output finite, 272 rows (the first, the last tile's 16 and an even
+    spread) against the f64 product, a second run bitwise equal.  The values
+    are 4 Mi N(0, 0.02) draws repeated over the table (as the bench)."""
+    n, k = 151936, 4096
+    values = np.resize(synth.normal(77, 1 << 22, 0.02), n * k)
+    data = ka.quantize(ka.Q6K, 0, values)
+    del values
+    w = ka.QuantizedTensor(dev(data), ka.Q6K, 0, n, k)
+    rb = ko.row_bytes(ka.Q6K, 0, k)
+    sample = np.unique(np.r_[np.linspace(0, n - 17, 256).astype(int), n - 16:n])
+    sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
+    for rows in (1, 8):
+        x = synth.normal(6 + rows, rows * k, 1.0).reshape(rows, k)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        assert got.shape == (rows, n) and np.isfinite(got).all()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        e64 = ko.product_f64([(ka.Q6K, 0, sub, len(sample))], k, x)
+        check_f32(got[:, sample], e64, f"table rows {rows}")
+
+
+def test_qwen3_8b_prefill_in_f32_at_full_size(hip):
+    """Config 4 in the reference's own mode above 16 rows (f32 products of
+    the bf16 activations, kapel-cpu/src/matmul.rs:303-306): the Q8_0 gate/up
+    and down calls at M = 512, a sample of 48 weight rows on 8 activation rows
+    against the f64 product within the bf16 output's rounding."""
+    rows = 512
+    calls = [((("gate", 12288), ("up", 12288)), 4096), ((("down", 4096),), 12288)]
+    for i, (call, k) in enumerate(calls):
+        mats = [synth_weight(ka.Q8_0, 0, n, k, 3100 + 10 * i + j) + (n,) for j, (_, n) in enumerate(call)]
+        xb = dev(synth.normal(21 + i, rows * k, 1.0).reshape(rows, k), torch.bfloat16)
+        got = hip.forward(ka.QuantizedMatmul(), [xb] + [m[1] for m in mats]).float().cpu().numpy()
+        assert np.isfinite(got).all()
+        x = xb.float().cpu().numpy()
+        pick = np.r_[0:4, rows - 4:rows]
+        col = 0
+        for data, _, n in mats:
+            sample = np.linspace(0, n - 1, 48).astype(int)
+            rb = ko.row_bytes(ka.Q8_0, 0, k)
+            sub = np.concatenate([data[r * rb:(r + 1) * rb] for r in sample])
+            e64 = ko.product_f64([(ka.Q8_0, 0, sub, len(sample))], k, x[pick])
+            have = got[pick][:, col + sample].astype(np.float64)
+            assert np.all(np.abs(have - e64) <= 2 ** -8 * np.abs(e64) + 1e-4 * (1 + np.abs(e64))), call
+            col += n
+
+
 def test_low_bit_mix_and_output_table_sample(hip):
-    """Config 5 shapes at M in {1, 8}: Q2_K/Q3_K/Q5_K FFN matrices, int4/32
-    attention, Q6_K output-table rows (a slice of 4096 rows of the table)."""
-    cases = [(ka.Q2K, 0, 12288, 4096), (ka.Q3K, 0, 4096, 12288), (ka.Q5K, 0, 12288, 4096),
-             (ka.INT4, 32, 4096, 4096), (ka.Q6K, 0, 4096, 4096)]
+    """Config 5 shapes at M in {1, 8}: the Q2_K, Q3_K and Q5_K FFN matrices
+    (up 12288 x 4096 and down 4096 x 12288 each), int4/32 attention (q and o
+    4096 x 4096, k and v 1024 x 4096), Q6_K output-table rows (a slice of
+    4096 rows of the table; the whole table has its own test)."""
+    cases = [(ka.Q2K, 0, 12288, 4096), (ka.Q2K, 0, 4096, 12288), (ka.Q3K, 0, 12288, 4096),
+             (ka.Q3K, 0, 4096, 12288), (ka.Q5K, 0, 12288, 4096), (ka.Q5K, 0, 4096, 12288),
+             (ka.INT4, 32, 4096, 4096), (ka.INT4, 32, 1024, 4096), (ka.Q6K, 0, 4096, 4096)]
     for i, (fmt, group, n, k) in enumerate(cases):
         data, w = synth_weight(fmt, group, n, k, 2000 + i)
         for rows in (1, 8):
@@ -342,7 +455,7 @@ def test_many_rows_of_every_format(hip, fmt, group):
         again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
         assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
         if byte:
-            hip.with_byte_activations(True)
+            hip.with_byte_activations(True, all_rows=True)
             try:
                 got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy().astype(np.float64)
             finally:
@@ -362,7 +475,7 @@ def test_qwen3_8b_prefill_at_full_size(hip):
     rows against the CPU algorithm (bytes.rs:200-241); every output is
     finite and a second run is bitwise equal."""
     rows = 512
-    hip.with_byte_activations(True)
+    hip.with_byte_activations(True, all_rows=True)
     try:
         mats = {name: synth_weight(ka.Q8_0, 0, n, k, 3000 + i) + (n, k)
                 for i, (name, n, k) in enumerate(QWEN3_8B)}
@@ -573,7 +686,7 @@ def test_outputs_written_in_full_and_workspace_reused(hip):
     xs = {rows: dev(x_uniform(rows, k, 400 + rows)) for rows in (1, 3, 17, 64)}
 
     def run(fmt, rows, byte):
-        hip.with_byte_activations(byte)
+        hip.with_byte_activations(byte, all_rows=byte)
         ws = [w for _, w in mats[fmt]]
         out = torch.full((rows, sum(w.n for w in ws)), float("nan"), device="cuda:0")
         hip.forward(ka.QuantizedMatmul(), [xs[rows]] + ws, out=out)

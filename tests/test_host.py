@@ -146,11 +146,12 @@ def test_workspace_grows_with_rows_and_covers_the_split():
     many = ka.lib().kh_qmatmul_workspace(arr, 1, 3072, 64, ka.BYTE_ACTIVATIONS)
     assert 0 < one < many
     assert ka.lib().kh_qmatmul_workspace(arr, 1, 3000, 1, 0) == 0  # refused: misaligned
-    # K = 0 (conformity.rs's [5, 0] case) is planned without a fault, at
-    # every row count and either activation kind.
+    # K = 0 (conformity.rs's [5, 0] case): the call plans no launch (the
+    # outputs are zero-filled), at every row count and activation kind; the
+    # workspace is still sized.
     empty = (ka._Weight * 1)(weight_struct(ka.Q4K, 0, 8, 0))
     for rows in (1, 3, 17, 64):
-        for flags in (0, ka.BYTE_ACTIVATIONS):
+        for flags in (0, ka.BYTE_ACTIVATIONS, ka.BYTE_ACTIVATIONS_ALL_ROWS):
             assert ka.lib().kh_qmatmul_workspace(empty, 1, 0, rows, flags) > 0
 
 
