@@ -127,6 +127,22 @@ int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_
                const void *x, uint64_t rows, uint32_t out_kind, void *out, uint32_t flags,
                void *workspace, uint64_t workspace_bytes, void *stream);
 
+/* kh_qmatmul without a workspace argument, for callers that cannot allocate
+ * (code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  The scratch is a
+ * file-scope device array of KH_STATIC_SCRATCH_BYTES on each device, held
+ * until the process ends; a call whose kh_qmatmul_workspace exceeds it is
+ * refused with KH_ERR_WORKSPACE before anything is launched.  It calls no
+ * hipMalloc or hipFree; the first call on a device clears the array's
+ * counters on its stream.  Every call on one device shares that device's
+ * array: calls that overlap on one device (two streams, two host threads)
+ * race, so they must be ordered; KH_REUSE_ACTIVATIONS reuses what the
+ * previous call on the device left in it. */
+#define KH_STATIC_SCRATCH_BYTES (32ull << 20)
+int kh_qmatmul_static(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
+                      const void *x, uint64_t rows, uint32_t out_kind, void *out, uint32_t flags,
+                      void *stream);
+
 /* Activations in bytes (kapel-cpu/src/bytes.rs:144-158): for each block of
  * 32, scale = max|x| / 127 and q = round-half-even(x * 127 / max) in
  * [-127, 127]; sums32 = scale * (sum of q).  q [rows, k] i8, scale and

@@ -89,7 +89,7 @@ _lib = None
 SYMBOLS = ("kh_version", "kh_error_string", "kh_block_len", "kh_block_bytes",
            "kh_qmatmul_workspace", "kh_qmatmul", "kh_quantize_x", "kh_block_dots",
            "kh_dequantize", "kh_dequantize_rows", "kh_quantize_host",
-           "kh_expert_matmul_workspace", "kh_expert_matmul")
+           "kh_expert_matmul_workspace", "kh_expert_matmul", "kh_qmatmul_static")
 
 
 def lib():
@@ -112,6 +112,7 @@ def lib():
     L.kh_qmatmul_workspace.argtypes = [W, u32, u64, u64, u32]
     L.kh_qmatmul_workspace.restype = u64
     L.kh_qmatmul.argtypes = [W, u32, u64, u32, P, u64, u32, P, u32, P, u64, P]
+    L.kh_qmatmul_static.argtypes = [W, u32, u64, u32, P, u64, u32, P, u32, P]
     L.kh_quantize_x.argtypes = [u32, P, u64, u64, P, P, P, P]
     L.kh_block_dots.argtypes = [W, u64, P, u64, P, P, u64, P]
     L.kh_dequantize.argtypes = [W, u64, u64, u64, u32, P, P]

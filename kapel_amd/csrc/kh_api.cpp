@@ -689,6 +689,62 @@ int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_
     return err == hipSuccess ? KH_OK : KH_ERR_HIP;
 }
 
+}  // extern "C"
+
+// The scratch of kh_qmatmul_static: one array per device, for callers that
+// cannot allocate.  Host code never names it after set-up: the array's
+// device address comes from hipGetSymbolAddress, once per device.
+static __device__ __align__(256) uint8_t scratch[KH_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+struct ScratchOf {
+    std::once_flag flag;
+    uint8_t *ptr = nullptr;
+    hipError_t err = hipSuccess;
+};
+ScratchOf scratch_of[MAX_DEVICES];
+
+// This device's copy of the array; the first call on the device also clears
+// its counters (on the caller's stream, by a fill kernel: no memset node for
+// a caller that captures the call in a graph).
+hipError_t device_scratch(hipStream_t s, uint8_t *&out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
+    ScratchOf &slot = scratch_of[dev];
+    std::call_once(slot.flag, [&] {
+        void *p = nullptr;
+        slot.err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (slot.err == hipSuccess) {
+            slot.ptr = static_cast<uint8_t *>(p);
+            slot.err = launch_fill(reinterpret_cast<uint32_t *>(slot.ptr), MAX_COUNTERS, s);
+        }
+    });
+    out = slot.ptr;
+    return slot.err;
+}
+
+}  // namespace
+
+extern "C" {
+
+int kh_qmatmul_static(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
+                      const void *x, uint64_t rows, uint32_t out_kind, void *out, uint32_t flags,
+                      void *stream) {
+    // The sizes are checked before anything touches the device.
+    const uint64_t need = kh_qmatmul_workspace(weights, count, k, rows, flags);
+    if (need > KH_STATIC_SCRATCH_BYTES) return KH_ERR_WORKSPACE;
+    // A refused call (its status from kh_qmatmul) touches no scratch.
+    if (need == 0) return kh_qmatmul(weights, count, k, x_kind, x, rows, out_kind, out, flags, nullptr, 0, stream);
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    uint8_t *ws = nullptr;
+    if (device_scratch(s, ws) != hipSuccess) return KH_ERR_HIP;
+    return kh_qmatmul(weights, count, k, x_kind, x, rows, out_kind, out, flags, ws, KH_STATIC_SCRATCH_BYTES,
+                      stream);
+}
+
 int kh_quantize_x(uint32_t x_kind, const void *x, uint64_t rows, uint64_t k, int8_t *q,
                   float *scale, float *sums32, void *stream) {
     if (!float_kind(x_kind)) return KH_ERR_DTYPE;

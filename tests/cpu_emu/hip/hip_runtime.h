@@ -317,6 +317,12 @@ typedef emu::BufferRsrc __amdgpu_buffer_rsrc_t;
 
 inline hipError_t hipGetLastError() { return hipSuccess; }
 enum hipFuncAttribute { hipFuncAttributeMaxDynamicSharedMemorySize = 8 };
+#define HIP_SYMBOL(X) X
+template <class T>
+inline hipError_t hipGetSymbolAddress(void **p, T &symbol) {
+    *p = (void *)&symbol;
+    return hipSuccess;
+}
 inline hipError_t hipGetDevice(int *dev) {
     *dev = 0;
     return hipSuccess;
