@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "../../include/kapel_hip.h"
@@ -46,7 +47,13 @@ inline hipError_t set_lds_limit(OncePerDevice &once, const void *kernel, int byt
     if (e != hipSuccess) return e;
     if (dev < 0 || dev >= MAX_DEVICES) return hipErrorInvalidDevice;
     std::call_once(once.flag[dev], [&] {
-        once.err[dev] = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        // At most what the kernel's static LDS (as rounded up by the
+        // compiler) leaves of a CU's 160 KiB.
+        hipFuncAttributes at;
+        once.err[dev] = hipFuncGetAttributes(&at, kernel);
+        if (once.err[dev] != hipSuccess) return;
+        once.err[dev] = hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                            std::min(bytes, 160 * 1024 - (int)at.sharedSizeBytes));
     });
     return once.err[dev];
 }

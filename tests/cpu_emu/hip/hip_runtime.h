@@ -327,6 +327,14 @@ inline hipError_t hipGetDevice(int *dev) {
     *dev = 0;
     return hipSuccess;
 }
+struct hipFuncAttributes {
+    size_t sharedSizeBytes;
+};
+// Static LDS is counted in the emulator's dynamic pool.
+inline hipError_t hipFuncGetAttributes(hipFuncAttributes *at, const void *) {
+    at->sharedSizeBytes = 0;
+    return hipSuccess;
+}
 inline hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int bytes) {
     return bytes <= (int)emu::LDS_BYTES ? hipSuccess : hipErrorInvalidValue;
 }
