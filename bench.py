@@ -16,7 +16,9 @@ call (28,311,552 weight bytes a launch), timed with HIP events around graph
 replays of that call alone on its stream; `traffic` comes from rocprofv3
 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/traffic.json.  `configs`
 holds the other BASELINE.json configurations (1, 3, 4, 5).  `cpu_baseline` is
-the oracle's f32 product (the restated kapel-cpu algorithm) on this host.
+kapel-cpu's AVX-512 product (restated in the oracle) on this host's cores, with
+a one-thread figure and its VNNI byte product at config 3.  Every GPU figure is
+the median of 3 timed graph replays.
 """
 import argparse
 import json
@@ -60,6 +62,66 @@ def physical_cores():
     allowed = len(os.sched_getaffinity(0))
     n = len(cores) if cores else allowed
     return max(1, min(n, allowed, 16))
+
+
+def cpu_baseline(args, host, layer_bytes, synth, with_bytes):
+    """kapel-cpu's products on this host's cores: its AVX-512 kernels
+    (quantized.rs:699-1021) restated in the oracle, on the config-2 layer at
+    M = 1, all cores and one thread; with `with_bytes`, its VNNI byte kernels
+    (bytes.rs:395-652) on the config-3 layer at M = 64.  Weight copies rotate
+    over more than 1 GB so that no pass is served from the host's caches.
+    Best of the timed passes, as kapel-cpu/examples/quantized.rs:14-27."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as ko
+
+    wide, vnni = ko.wide_available()
+    copies = max(2, -(-(1 << 30) // layer_bytes))
+    sets = [[[(host[c][0], 0, np.copy(host[c][1]), host[c][2]) for c in call] for call in CALLS]
+            for _ in range(copies)]
+    cx = [synth.normal(7 + ci, host[call[0]][3], 1.0).reshape(1, -1) for ci, call in enumerate(CALLS)]
+    product = ko.product_wide if wide else ko.product_f32
+
+    def passes(fn, seconds, most=1000):
+        best, times, i = float("inf"), [], 0
+        fn(0)
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end and i < most:
+            t0 = time.perf_counter()
+            fn(i)
+            times.append(time.perf_counter() - t0)
+            i += 1
+        return min(times), len(times), sum(times)
+
+    def layer(threads):
+        def run(i):
+            for ci, call in enumerate(CALLS):
+                product(sets[i % copies][ci], host[call[0]][3], cx[ci], threads)
+        return run
+
+    threads = physical_cores()
+    best, n_all, el_all = passes(layer(threads), args.cpu_seconds * 0.5)
+    best1, n_one, el_one = passes(layer(1), args.cpu_seconds * 0.5)
+    kind = "restated AVX-512 wide::fused" if wide else "portable loop (no AVX-512 on this host)"
+    cpu = {"value": round(layer_bytes / best / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+           "variant": "restated-avx512" if wide else "portable",
+           "value_1thread": round(layer_bytes / best1 / 1e9, 2),
+           "sample": f"config-2 layer (63.1 MB, M = 1, f32 x), {kind}: best of {n_all} passes on "
+                     f"{threads} threads ({el_all:.1f} s) and of {n_one} on 1 thread ({el_one:.1f} s), "
+                     f"{copies} weight copies rotated"}
+    if with_bytes and vnni:
+        xs = [synth.normal(7 + ci, 64 * host[call[0]][3], 1.0).reshape(64, -1) for ci, call in enumerate(CALLS)]
+        prepared = [ko.quantize_x(x) for x in xs]
+
+        def layer64(i):
+            for ci, call in enumerate(CALLS):
+                ko.product_vnni(sets[i % copies][ci], host[call[0]][3], threads=threads, prepared=prepared[ci])
+        b64, n64, el64 = passes(layer64, args.cpu_seconds * 0.5)
+        ops = 2 * 64 * sum(n * k for _, n, k, _ in LAYER)
+        cpu["config3"] = {"ms_per_layer": round(b64 * 1e3, 3), "tops": round(ops / b64 / 1e12, 4),
+                          "sample": f"config-3 layer at M = 64 in bytes, restated AVX-512 VNNI kernels, "
+                                    f"best of {n64} passes on {threads} threads ({el64:.1f} s)"}
+    return cpu
 
 
 def main():
@@ -147,35 +209,42 @@ def main():
         return xs, outs
 
     def reserve(calls, layer, rows, byte):
+        """The workspace of the largest call (byte activations at every row
+        count with `byte`)."""
         size = 0
         for call in calls:
             ws = [layer[c] for c in call]
             arr = (ka._Weight * len(ws))(*[w.weight() for w in ws])
             size = max(size, ka.lib().kh_qmatmul_workspace(
-                arr, len(ws), ws[0].k, rows, ka.BYTE_ACTIVATIONS if byte else 0))
+                arr, len(ws), ws[0].k, rows, ka.BYTE_ACTIVATIONS_ALL_ROWS if byte else 0))
         hip.workspace(size)
 
-    def timed(step_fns, steps, warmup):
-        """Graph of len(step_fns) steps, checked against an eager run, then
-        `steps` steps timed with events; seconds per step."""
-        n = len(step_fns)
-        step_fns[-1]()
+    def timed(step_fns, steps, warmup, replays=3):
+        """One HIP graph of `steps` steps (step i runs step_fns[i % len]),
+        checked against an eager run; `warmup` steps' worth of untimed
+        replays, then `replays` replays, each bracketed by synchronizations
+        and timed with events on the capture stream.  Seconds per step (the
+        median replay) and the per-replay figures."""
+        steps = max(1, steps)
+        step_fns[(steps - 1) % len(step_fns)]()
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            for fn in step_fns:
-                fn()
-        for _ in range(max(1, warmup // n)):
+            for i in range(steps):
+                step_fns[i % len(step_fns)]()
+        for _ in range(max(1, -(-warmup // steps))):
             g.replay()
         torch.cuda.synchronize()
-        reps = max(1, steps // n)
-        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        a.record()
-        for _ in range(reps):
+        per = []
+        for _ in range(max(3, replays)):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
             g.replay()
-        b.record()
-        torch.cuda.synchronize()
-        return a.elapsed_time(b) * 1e-3 / (reps * n), reps * n
+            b.record()
+            torch.cuda.synchronize()
+            per.append(a.elapsed_time(b) * 1e-3 / steps)
+        return sorted(per)[len(per) // 2], per
 
     # ---- config 2: the layer at M = 1 (value) ----------------------------------
     hip.with_byte_activations(False)
@@ -189,10 +258,10 @@ def main():
         return run
 
     # Graph replays agree with the eager product, bit for bit.
-    layer_step(L - 1)()
+    layer_step((args.steps - 1) % L)()
     torch.cuda.synchronize()
     eager = [o.clone() for o in outs]
-    sec, steps_done = timed([layer_step(l) for l in range(L)], args.steps, args.warmup)
+    sec, per_replay = timed([layer_step(l) for l in range(L)], args.steps, args.warmup)
     for a_, b_ in zip(outs, eager):
         assert torch.equal(a_, b_), "graph replay differs from the eager product"
     value = layer_bytes / sec / 1e9
@@ -216,14 +285,16 @@ def main():
                 "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                 "algorithmic_bytes_per_launch": gate_bytes,
                 "avg_launch_us": round(gsec * 1e6, 2),
-                "timing": "HIP events around graph replays of 28 launches (rotated weights)"}
+                "timing": "HIP events around graph replays of 280 launches over 28 rotated weight "
+                          "copies, median of 3 replays"}
 
     configs = {}
     only = set() if args.no_configs else set(args.configs.split(","))
     if only:
         if "3" in only:
-            # ---- config 3: the same layer, M = 64, byte activations ---------------
-            hip.with_byte_activations(True)
+            # ---- config 3: the same layer, M = 64, byte activations at every
+            # row count (the reference's CPU takes bytes up to 16 rows only)
+            hip.with_byte_activations(True, all_rows=True)
             reserve(CALLS, layers[0], 64, True)
             xs, outs = inputs_for(CALLS, host, 64)
             s3, _ = timed([layer_step(l) for l in range(L)], 2 * L, L)
@@ -283,7 +354,7 @@ def main():
             qhost, qbytes = quantized_layer(QWEN_LAYER, 300, lambda r: ka.Q8_0)
             qlayers = [{name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
                         for name, (fmt, data, n, k) in qhost.items()} for _ in range(2)]
-            hip.with_byte_activations(True)
+            hip.with_byte_activations(True, all_rows=True)
             reserve(QWEN_CALLS, qlayers[0], 512, True)
             xq, oq = inputs_for(QWEN_CALLS, qhost, 512, dtype=torch.bfloat16)
 
@@ -296,10 +367,18 @@ def main():
             s4, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
             hip.with_byte_activations(False)
             ops4 = 2 * 512 * sum(n * k for _, n, k in QWEN_LAYER)
+            # The reference's own arithmetic at 512 rows: activations as they
+            # are (three fixed-point byte planes here, exact to 2^-23).
+            reserve(QWEN_CALLS, qlayers[0], 512, False)
+            s4f, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
             configs["4"] = {"workload": "Qwen3-8B layer in Q8_0, M = 512, bf16 activations quantized to bytes",
                             "ms_per_step": round(s4 * 1e3, 3), "tops": round(ops4 / s4 / 1e12, 2),
                             "mfma_frac": round(ops4 / s4 / 1e12 / INT8_PEAK_TOPS, 4),
-                            "weight_gbps": round(qbytes / s4 / 1e9, 1)}
+                            "weight_gbps": round(qbytes / s4 / 1e9, 1),
+                            "bf16_activations": {"ms_per_step": round(s4f * 1e3, 3),
+                                                 "tops": round(ops4 / s4f / 1e12, 2),
+                                                 "note": "activations not rounded to bytes (the drop-in "
+                                                         "default above 16 rows): 3 int8 planes a row"}}
             del qlayers
 
         if "moe" in only:
@@ -340,33 +419,16 @@ def main():
 
     cpu = None
     if not args.no_cpu:
-        sys.path.insert(0, os.path.join(ROOT, "oracle"))
-        import oracle as ko
-        threads = physical_cores()
-        parts = [[(host[c][0], 0, host[c][1], host[c][2]) for c in call] for call in CALLS]
-        cx = [synth.normal(7 + ci, host[call[0]][3], 1.0).reshape(1, -1)
-              for ci, call in enumerate(CALLS)]
-        for ci in range(len(CALLS)):
-            ko.product_f32(parts[ci], host[CALLS[ci][0]][3], cx[ci], threads)
-        passes, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < args.cpu_seconds:
-            for ci in range(len(CALLS)):
-                ko.product_f32(parts[ci], host[CALLS[ci][0]][3], cx[ci], threads)
-            passes += 1
-        el = time.perf_counter() - t0
-        cpu = {"value": round(layer_bytes * passes / el / 1e9, 2), "unit": "GB/s",
-               "cores": threads, "kind": "port",
-               "sample": f"{passes} passes of the config-2 layer (63.1 MB) at M = 1, "
-                         f"f32 activations, {el:.1f} s, the oracle's threaded restatement of "
-                         "kapel-cpu's portable quantized product"}
+        cpu = cpu_baseline(args, host, layer_bytes, synth, "3" in only)
 
     line = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1,
-            "steps": steps_done, "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4),
+            "steps": max(1, args.steps), "warmup": args.warmup, "ms_per_step": round(sec * 1e3, 4),
             "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
             "dtype": "int8 (i8 x i8 -> i32 MFMA dots, f32 scales)", "data": "synthetic",
             "config": {"workload": "config 2: Llama-3.2-3B decode layer, Q4_K (q, k, v, o, "
                                    "gate, up) + Q6_K (down), M = 1, f32 activations",
                        "weight_bytes_per_step": layer_bytes, "layers_rotated": L,
+                       "ms_per_step_replays": [round(t * 1e3, 4) for t in per_replay],
                        "frac_of_hbm_peak": round(value / HBM_PEAK_GBPS, 4)},
             "roofline": roofline, "configs": configs, "cpu_baseline": cpu}
     print(json.dumps(line), flush=True)

@@ -34,6 +34,7 @@
 #include <stdlib.h>
 #include <string.h>
 #include <pthread.h>
+#include <immintrin.h>
 
 /* Format codes: those of kapel-cuda-abi/src/lib.rs:167-194, plus Q2_K = 13,
  * Q3_K = 14 (the reference's ABI has no code for them). */
@@ -776,6 +777,7 @@ typedef struct {
     const float *x;
     float *out;
     int bytes_mode;
+    int wide;               /* the AVX-512 (f32) / AVX-512 VNNI (bytes) kernels */
     /* byte mode inputs */
     const int8_t *q;
     const float *scale;
@@ -787,6 +789,8 @@ typedef struct {
 
 static void product_task(ko_job *job, const ko_task *t);
 static void bytes_task(ko_job *job, const ko_task *t);
+static void wide_task(ko_job *job, const ko_task *t);
+static void vnni_task(ko_job *job, const ko_task *t);
 
 static void *worker(void *arg) {
     ko_job *job = arg;
@@ -795,8 +799,8 @@ static void *worker(void *arg) {
         int64_t i = job->next++;
         pthread_mutex_unlock(&job->lock);
         if (i >= job->ntasks) return NULL;
-        if (job->bytes_mode) bytes_task(job, &job->tasks[i]);
-        else product_task(job, &job->tasks[i]);
+        if (job->bytes_mode) (job->wide ? vnni_task : bytes_task)(job, &job->tasks[i]);
+        else (job->wide ? wide_task : product_task)(job, &job->tasks[i]);
     }
 }
 
@@ -1080,5 +1084,355 @@ int ko_product_f64(int count, const int *fmts, const int *groups, const uint8_t 
         }
     }
     free(w);
+    return 0;
+}
+
+/* ---------------------------------------------------------------------- */
+/* The AVX-512 kernels kapel-cpu runs on a processor that has them: the    */
+/* timed CPU baseline.  f32 activations: quantized.rs:699-1021 (`wide`),   */
+/* rows by 8, 4, 2, 1 (:711-731); bytes: bytes.rs:395-652 (`vnni`), views  */
+/* of up to 4 rows (bytes.rs:38, :411-418).  Formats Q4_0, Q8_0, Q4_K and  */
+/* Q6_K (the benchmark's); the tasks and the thread split are those of the */
+/* portable products above.                                                 */
+/* ---------------------------------------------------------------------- */
+
+#define WIDE __attribute__((target("avx512f,avx512bw,avx512dq,avx512vl,avx2,fma")))
+#define VNNI __attribute__((target("avx512f,avx512bw,avx512dq,avx512vl,avx512vnni,avx2,fma")))
+#define INLINE static inline __attribute__((always_inline))
+
+/* An f16 scale as f32 (exact), by F16C: no call in the loops. */
+WIDE INLINE float w_half(const uint8_t *b, int at) {
+    uint16_t h;
+    memcpy(&h, b + at, 2);
+    return _cvtsh_ss(h);
+}
+
+/* Bit 0: AVX-512 F/BW/DQ/VL; bit 1: also VNNI (isa.rs:20-35, bytes.rs:89). */
+int ko_wide_available(void) {
+    __builtin_cpu_init();
+    int wide = __builtin_cpu_supports("avx512f") && __builtin_cpu_supports("avx512bw") &&
+               __builtin_cpu_supports("avx512dq") && __builtin_cpu_supports("avx512vl") &&
+               __builtin_cpu_supports("fma");
+    return wide ? 1 | (__builtin_cpu_supports("avx512vnni") ? 2 : 0) : 0;
+}
+
+static int wide_format(int fmt) {
+    return fmt == KO_Q4_0 || fmt == KO_Q8_0 || fmt == KO_Q4K || fmt == KO_Q6K;
+}
+
+/* quantized.rs:980-1011 */
+WIDE INLINE __m128i w_bytes(const uint8_t *b) { return _mm_loadu_si128((const __m128i *)b); }
+WIDE INLINE __m128i w_take(__m128i v, int shift, char mask) {
+    return _mm_and_si128(_mm_srl_epi16(v, _mm_cvtsi64_si128(shift)), _mm_set1_epi8(mask));
+}
+WIDE INLINE __m512 w_unsigned(__m128i v) { return _mm512_cvtepi32_ps(_mm512_cvtepu8_epi32(v)); }
+WIDE INLINE __m512 w_signed(__m128i v) { return _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(v)); }
+
+/* Codes 16 s ... 16 s + 15 of a block as floats (quantized.rs:779-899). */
+WIDE INLINE __m512 w_codes(int fmt, const uint8_t *b, int s) {
+    switch (fmt) {
+    case KO_Q8_0: return w_signed(w_bytes(b + 2 + 16 * s));
+    case KO_Q4_0: return w_signed(_mm_sub_epi8(w_take(w_bytes(b + 2), 4 * s, 0x0f), _mm_set1_epi8(8)));
+    case KO_Q4K: {
+        int c = s / 4, high = s % 4 / 2, part = s % 2;
+        return w_unsigned(w_take(w_bytes(b + 16 + c * 32 + part * 16), 4 * high, 0x0f));
+    }
+    default: { /* Q6_K */
+        int h = s / 8, shift = s % 8 / 2, part = s % 2;
+        __m128i ql = w_take(w_bytes(b + h * 64 + (shift % 2) * 32 + part * 16), 4 * (shift / 2), 0x0f);
+        __m128i qh = w_take(w_bytes(b + 128 + h * 32 + part * 16), 2 * shift, 3);
+        __m128i q = _mm_or_si128(ql, _mm_slli_epi16(qh, 4));
+        return w_signed(_mm_sub_epi8(q, _mm_set1_epi8(32)));
+    }
+    }
+}
+
+/* k_scales32 (quantized.rs:603-617) with the scales converted inline. */
+WIDE INLINE void w_k_scales(const uint8_t *block, float *scale, float *minimum) {
+    float d = w_half(block, 0), dmin = w_half(block, 2);
+    const uint8_t *sc = block + 4, *mn = block + 8, *md = block + 12;
+    for (int i = 0; i < 4; i++) {
+        scale[i] = d * (float)(sc[i] & 0x3f);
+        minimum[i] = dmin * (float)(mn[i] & 0x3f);
+        scale[4 + i] = d * (float)((md[i] & 0x0f) | ((sc[i] >> 2) & 0x30));
+        minimum[4 + i] = dmin * (float)((md[i] >> 4) | ((mn[i] >> 2) & 0x30));
+    }
+}
+
+/* The scales (and minimums) of a block's groups. */
+WIDE INLINE void w_scales(int fmt, const uint8_t *b, float *scale, float *minimum) {
+    switch (fmt) {
+    case KO_Q8_0: case KO_Q4_0: scale[0] = w_half(b, 0); minimum[0] = 0.0f; break;
+    case KO_Q4K: w_k_scales(b, scale, minimum); break;
+    default: {
+        __m512 d = _mm512_set1_ps(w_half(b, 208));
+        _mm512_storeu_ps(scale, _mm512_mul_ps(w_signed(w_bytes(b + 192)), d));
+    }
+    }
+}
+
+/* quantized.rs:914-975: out[r * count + j] = x[r] . w[j] for R rows. */
+WIDE INLINE void w_fused(int fmt, int R, const uint8_t *w, int64_t k, const float *x, int64_t count,
+                         float *out) {
+    const int LEN = fmt == KO_Q4K || fmt == KO_Q6K ? 256 : 32;
+    const int BYTES = fmt == KO_Q8_0 ? 34 : fmt == KO_Q4_0 ? 18 : fmt == KO_Q4K ? 144 : 210;
+    const int GROUP = fmt == KO_Q6K ? 16 : 32;
+    const int MIN = fmt == KO_Q4K;
+    const int64_t blocks = k / LEN, groups = k / GROUP;
+    float *sums = NULL;
+    if (MIN) {
+        sums = malloc(sizeof(float) * (size_t)(R * groups));
+        for (int r = 0; r < R; r++)
+            for (int64_t g = 0; g < groups; g++) {
+                float lanes[LANES] = {0};
+                const float *v = x + r * k + g * GROUP;
+                for (int i = 0; i < GROUP; i++) lanes[i % LANES] += v[i];
+                sums[r * groups + g] = reduce16(lanes);
+            }
+    }
+    float scale[16], minimum[16];
+    for (int64_t j = 0; j < count; j++) {
+        const uint8_t *row = w + j * blocks * BYTES;
+        __m512 acc[8];
+        float low[8];
+        for (int r = 0; r < R; r++) { acc[r] = _mm512_setzero_ps(); low[r] = 0.0f; }
+        for (int64_t b = 0; b < blocks; b++) {
+            const uint8_t *block = row + b * BYTES;
+            w_scales(fmt, block, scale, minimum);
+#pragma GCC unroll 16
+            for (int g = 0; g < LEN / GROUP; g++) {
+                __m512 t[8];
+                for (int r = 0; r < R; r++) t[r] = _mm512_setzero_ps();
+#pragma GCC unroll 2
+                for (int s = 0; s < GROUP / 16; s++) {
+                    __m512 q = w_codes(fmt, block, g * GROUP / 16 + s);
+                    for (int r = 0; r < R; r++) {
+                        __m512 v = _mm512_loadu_ps(x + r * k + b * LEN + g * GROUP + s * 16);
+                        t[r] = _mm512_fmadd_ps(q, v, t[r]);
+                    }
+                }
+                __m512 sc = _mm512_set1_ps(scale[g]);
+                for (int r = 0; r < R; r++) acc[r] = _mm512_fmadd_ps(t[r], sc, acc[r]);
+                if (MIN)
+                    for (int r = 0; r < R; r++) low[r] += minimum[g] * sums[r * groups + b * (LEN / GROUP) + g];
+            }
+        }
+        for (int r = 0; r < R; r++) out[r * count + j] = _mm512_reduce_add_ps(acc[r]) - low[r];
+    }
+    free(sums);
+}
+
+/* One instance per format and row count, as the reference's generics. */
+#define W_INST(F, R) \
+    WIDE static void w_##F##_##R(const uint8_t *w, int64_t k, const float *x, int64_t n, float *o) { \
+        w_fused(KO_##F, R, w, k, x, n, o); \
+    }
+#define W_ROWS(F) W_INST(F, 1) W_INST(F, 2) W_INST(F, 4) W_INST(F, 8)
+W_ROWS(Q8_0) W_ROWS(Q4_0) W_ROWS(Q4K) W_ROWS(Q6K)
+
+WIDE static void w_rows(int fmt, const uint8_t *w, int64_t k, const float *x, int R, int64_t count,
+                        float *out) {
+#define W_PICK(F) \
+    (R == 8 ? w_##F##_8 : R == 4 ? w_##F##_4 : R == 2 ? w_##F##_2 : w_##F##_1)
+    void (*f)(const uint8_t *, int64_t, const float *, int64_t, float *) =
+        fmt == KO_Q8_0 ? W_PICK(Q8_0) : fmt == KO_Q4_0 ? W_PICK(Q4_0) : fmt == KO_Q4K ? W_PICK(Q4K) : W_PICK(Q6K);
+    f(w, k, x, count, out);
+#undef W_PICK
+}
+
+/* quantized.rs:151-174 with wide::rows (:711-731). */
+static void wide_task(ko_job *job, const ko_task *t) {
+    const ko_weights *w = &job->w[t->matrix];
+    int len = ko_block_len(w->fmt, w->group), size = ko_block_bytes(w->fmt, w->group);
+    int64_t k = job->k, row_bytes = k / len * size;
+    const uint8_t *bytes = w->bytes + t->first * row_bytes;
+    float *part = malloc(sizeof(float) * (size_t)(job->rows * t->count + 1));
+    for (int64_t first = 0; first < job->rows;) {
+        int64_t left = job->rows - first;
+        int R = left >= 8 ? 8 : left >= 4 ? 4 : left >= 2 ? 2 : 1;
+        w_rows(w->fmt, bytes, k, job->x + first * k, R, t->count, part + first * t->count);
+        first += R;
+    }
+    for (int64_t r = 0; r < job->rows; r++)
+        memcpy(job->out + r * job->width + t->column, part + r * t->count,
+               sizeof(float) * (size_t)t->count);
+    free(part);
+}
+
+/* ko_product_f32 with the AVX-512 kernels.  -2: no AVX-512 here or a format
+ * they do not take. */
+int ko_wide_product_f32(int count, const int *fmts, const int *groups, const uint8_t *const *ptrs,
+                        const int64_t *ns, int64_t k, const float *x, int64_t rows, float *out,
+                        int threads) {
+    ko_weights w[64];
+    if (count > 64) return -1;
+    if (!(ko_wide_available() & 1)) return -2;
+    int64_t width = 0;
+    for (int i = 0; i < count; i++) {
+        if (!wide_format(fmts[i])) return -2;
+        w[i].fmt = fmts[i]; w[i].group = groups[i]; w[i].bytes = ptrs[i]; w[i].n = ns[i];
+        if (k % ko_block_len(fmts[i], groups[i])) return -1;
+        width += ns[i];
+    }
+    if (width == 0 || rows == 0) return 0;
+    if (k == 0) { memset(out, 0, sizeof(float) * (size_t)(rows * width)); return 0; }
+    int64_t nt;
+    ko_task *tasks = make_tasks(threads < 1 ? 1 : threads, w, count, k, &nt);
+    ko_job job = {.w = w, .tasks = tasks, .ntasks = nt, .k = k, .rows = rows, .width = width,
+                  .x = x, .out = out, .bytes_mode = 0, .wide = 1};
+    run_job(&job, threads);
+    free(tasks);
+    return 0;
+}
+
+/* bytes.rs:420-452 */
+VNNI INLINE __m256i v_load32(const void *b) { return _mm256_loadu_si256((const __m256i *)b); }
+VNNI INLINE __m128i v_load16(const void *b) { return _mm_loadu_si128((const __m128i *)b); }
+VNNI INLINE __m256i v_take(__m256i v, int shift, char mask) {
+    return _mm256_and_si256(_mm256_srl_epi16(v, _mm_cvtsi64_si128(shift)), _mm256_set1_epi8(mask));
+}
+VNNI INLINE __m128i v_take16(__m128i v, int shift, char mask) {
+    return _mm_and_si128(_mm_srl_epi16(v, _mm_cvtsi64_si128(shift)), _mm_set1_epi8(mask));
+}
+/* bytes.rs:641-648: the sum of eight lanes, pairwise. */
+VNNI INLINE float v_reduce(__m256 v) {
+    __m128 quad = _mm_add_ps(_mm256_castps256_ps128(v), _mm256_extractf128_ps(v, 1));
+    __m128 pair = _mm_add_ps(quad, _mm_movehl_ps(quad, quad));
+    return _mm_cvtss_f32(_mm_add_ss(pair, _mm_movehdup_ps(pair)));
+}
+
+/* Codes 32 c ... 32 c + 31 of a block as bytes (bytes.rs:488-537). */
+VNNI INLINE __m256i v_codes(int fmt, const uint8_t *b, int c) {
+    switch (fmt) {
+    case KO_Q8_0: return v_load32(b + 2);
+    case KO_Q4_0: {
+        __m128i v = v_load16(b + 2);
+        return _mm256_set_m128i(v_take16(v, 4, 0x0f), v_take16(v, 0, 0x0f));
+    }
+    case KO_Q4K: return v_take(v_load32(b + 16 + c / 2 * 32), 4 * (c % 2), 0x0f);
+    default: { /* Q6_K */
+        int h = c / 4, s = c % 4;
+        __m256i ql = v_take(v_load32(b + h * 64 + (s % 2) * 32), 4 * (s / 2), 0x0f);
+        __m256i qh = v_take(v_load32(b + 128 + h * 32), 2 * s, 3);
+        return _mm256_sub_epi8(_mm256_or_si256(ql, _mm256_slli_epi16(qh, 4)), _mm256_set1_epi8(32));
+    }
+    }
+}
+
+VNNI INLINE void v_scales(int fmt, const uint8_t *b, float *scale, float *minimum) {
+    switch (fmt) {
+    case KO_Q8_0: scale[0] = w_half(b, 0); minimum[0] = 0.0f; break;
+    case KO_Q4_0: scale[0] = w_half(b, 0); minimum[0] = 8.0f * scale[0]; break;
+    case KO_Q4K: w_k_scales(b, scale, minimum); break;
+    default: {
+        __m512 s = _mm512_cvtepi32_ps(_mm512_cvtepi8_epi32(v_load16(b + 192)));
+        _mm512_storeu_ps(scale, _mm512_mul_ps(s, _mm512_set1_ps(w_half(b, 208))));
+    }
+    }
+}
+
+/* bytes.rs:557-638: R rows of byte activations (q, scale, sums32 of the
+ * job, rows r0 ...), signed codes by vpdpbusd with the signs moved to the
+ * activations. */
+VNNI INLINE void v_fused(int fmt, int R, const uint8_t *w, const ko_job *job, int64_t r0, int64_t count,
+                         float *out) {
+    const int LEN = fmt == KO_Q4K || fmt == KO_Q6K ? 256 : 32;
+    const int BYTES = fmt == KO_Q8_0 ? 34 : fmt == KO_Q4_0 ? 18 : fmt == KO_Q4K ? 144 : 210;
+    const int GROUP = fmt == KO_Q6K ? 16 : 32;
+    const int SIGNED = fmt == KO_Q8_0 || fmt == KO_Q6K, MIN = fmt == KO_Q4_0 || fmt == KO_Q4K;
+    const int64_t k = job->k, blocks = k / LEN;
+    float scale[16], minimum[16];
+    for (int64_t j = 0; j < count; j++) {
+        const uint8_t *row = w + j * blocks * BYTES;
+        __m256 acc[4], lows[4];
+        float low[4];
+        for (int r = 0; r < R; r++) { acc[r] = lows[r] = _mm256_setzero_ps(); low[r] = 0.0f; }
+        for (int64_t b = 0; b < blocks; b++) {
+            const uint8_t *block = row + b * BYTES;
+            v_scales(fmt, block, scale, minimum);
+#pragma GCC unroll 8
+            for (int c = 0; c < LEN / BLOCK; c++) {
+                __m256 factor = GROUP >= BLOCK ? _mm256_set1_ps(scale[c * BLOCK / GROUP])
+                                               : _mm256_set_m128(_mm_set1_ps(scale[2 * c + 1]),
+                                                                 _mm_set1_ps(scale[2 * c]));
+                __m256i u = v_codes(fmt, block, c), sign = _mm256_setzero_si256();
+                if (SIGNED) { sign = u; u = _mm256_abs_epi8(u); }
+                for (int r = 0; r < R; r++) {
+                    int64_t at = b * LEN + c * BLOCK, row_at = (r0 + r) * k;
+                    __m256i xq = v_load32(job->q + row_at + at);
+                    if (SIGNED) xq = _mm256_sign_epi8(xq, sign);
+                    __m256i dot = _mm256_dpbusd_epi32(_mm256_setzero_si256(), u, xq);
+                    __m256 f = _mm256_mul_ps(factor, _mm256_set1_ps(job->scale[(row_at + at) / BLOCK]));
+                    acc[r] = _mm256_fmadd_ps(_mm256_cvtepi32_ps(dot), f, acc[r]);
+                }
+            }
+            if (MIN && LEN / GROUP == 8) {
+                __m256 m = _mm256_loadu_ps(minimum);
+                for (int r = 0; r < R; r++)
+                    lows[r] = _mm256_fmadd_ps(m, _mm256_loadu_ps(job->sums32 + ((r0 + r) * k) / BLOCK + b * 8),
+                                              lows[r]);
+            } else if (MIN) {
+                for (int r = 0; r < R; r++)
+                    for (int g = 0; g < LEN / GROUP; g++)
+                        low[r] += minimum[g] * job->sums32[((r0 + r) * k) / BLOCK + b * (LEN / GROUP) + g];
+            }
+        }
+        for (int r = 0; r < R; r++) out[r * count + j] = v_reduce(acc[r]) - (low[r] + v_reduce(lows[r]));
+    }
+}
+
+#define V_INST(F, R) \
+    VNNI static void v_##F##_##R(const uint8_t *w, const ko_job *j, int64_t r0, int64_t n, float *o) { \
+        v_fused(KO_##F, R, w, j, r0, n, o); \
+    }
+#define V_ROWS(F) V_INST(F, 1) V_INST(F, 2) V_INST(F, 3) V_INST(F, 4)
+V_ROWS(Q8_0) V_ROWS(Q4_0) V_ROWS(Q4K) V_ROWS(Q6K)
+
+/* bytes.rs:200-241 with vnni::rows (:411-418). */
+static void vnni_task(ko_job *job, const ko_task *t) {
+    const ko_weights *w = &job->w[t->matrix];
+    int len = ko_block_len(w->fmt, w->group), size = ko_block_bytes(w->fmt, w->group);
+    int64_t k = job->k, row_bytes = k / len * size;
+    const uint8_t *bytes = w->bytes + t->first * row_bytes;
+    float *part = malloc(sizeof(float) * (size_t)(job->rows * t->count + 1));
+#define V_PICK(F) \
+    (R == 4 ? v_##F##_4 : R == 3 ? v_##F##_3 : R == 2 ? v_##F##_2 : v_##F##_1)
+    for (int64_t r0 = 0; r0 < job->rows; r0 += BROWS) {
+        int R = job->rows - r0 < BROWS ? (int)(job->rows - r0) : BROWS;
+        void (*f)(const uint8_t *, const ko_job *, int64_t, int64_t, float *) =
+            w->fmt == KO_Q8_0 ? V_PICK(Q8_0) : w->fmt == KO_Q4_0 ? V_PICK(Q4_0)
+                              : w->fmt == KO_Q4K ? V_PICK(Q4K) : V_PICK(Q6K);
+        f(bytes, job, r0, t->count, part + r0 * t->count);
+    }
+#undef V_PICK
+    for (int64_t r = 0; r < job->rows; r++)
+        memcpy(job->out + r * job->width + t->column, part + r * t->count,
+               sizeof(float) * (size_t)t->count);
+    free(part);
+}
+
+/* ko_product_bytes with the VNNI kernels; sums32 as ko_quantize_x writes
+ * them.  -2: no AVX-512 VNNI here or a format they do not take. */
+int ko_vnni_product_bytes(int count, const int *fmts, const int *groups, const uint8_t *const *ptrs,
+                          const int64_t *ns, int64_t k, const int8_t *q, const float *scale,
+                          const float *sums32, int64_t rows, float *out, int threads) {
+    ko_weights w[64];
+    if (count > 64) return -1;
+    if (!(ko_wide_available() & 2)) return -2;
+    int64_t width = 0;
+    for (int i = 0; i < count; i++) {
+        if (!wide_format(fmts[i])) return -2;
+        if (k % ko_block_len(fmts[i], groups[i])) return -1;
+        w[i].fmt = fmts[i]; w[i].group = groups[i]; w[i].bytes = ptrs[i]; w[i].n = ns[i];
+        width += ns[i];
+    }
+    if (width == 0 || rows == 0) return 0;
+    if (k == 0) { memset(out, 0, sizeof(float) * (size_t)(rows * width)); return 0; }
+    int64_t nt;
+    ko_task *tasks = make_tasks(threads < 1 ? 1 : threads, w, count, k, &nt);
+    ko_job job = {.w = w, .tasks = tasks, .ntasks = nt, .k = k, .rows = rows, .width = width,
+                  .out = out, .bytes_mode = 1, .wide = 1, .q = q, .scale = scale, .sums32 = sums32};
+    run_job(&job, threads);
+    free(tasks);
     return 0;
 }

@@ -48,6 +48,9 @@ def lib():
         L.ko_bytes_layout.argtypes = [i32, i32, P, P, P, P]
         L.ko_iq_table.argtypes = [i32, i32]
         L.ko_iq_table.restype = i64
+        L.ko_wide_available.argtypes = []
+        L.ko_wide_product_f32.argtypes = [i32, P, P, P, P, i64, P, i64, P, i32]
+        L.ko_vnni_product_bytes.argtypes = [i32, P, P, P, P, i64, P, P, P, i64, P, i32]
         _lib = L
     return _lib
 
@@ -144,6 +147,46 @@ def product_f64(weights, k, x):
     out = np.zeros((x.shape[0], int(ns.sum())), dtype=np.float64)
     rc = lib().ko_product_f64(count, _p(fmts), _p(groups), _p(ptrs), _p(ns), k, _p(x), x.shape[0],
                               _p(out))
+    assert rc == 0, rc
+    return out
+
+
+def wide_available():
+    """(AVX-512, AVX-512 VNNI) on this host, as kapel-cpu detects them
+    (kapel-cpu/src/isa.rs:20-35, bytes.rs:89)."""
+    bits = lib().ko_wide_available()
+    return bool(bits & 1), bool(bits & 2)
+
+
+WIDE_FORMATS = (Q8_0, Q4_0, Q4K, Q6K)  # the formats of the restated AVX-512 kernels
+
+
+def product_wide(weights, k, x, threads=1):
+    """kapel-cpu's product with its AVX-512 kernels (quantized.rs:699-1021,
+    `wide::fused`), f32 activations; None where this host or a format does
+    not take them."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, k)
+    count, fmts, groups, datas, ptrs, ns = _weights(weights)
+    out = np.zeros((x.shape[0], int(ns.sum())), dtype=np.float32)
+    rc = lib().ko_wide_product_f32(count, _p(fmts), _p(groups), _p(ptrs), _p(ns), k, _p(x),
+                                   x.shape[0], _p(out), threads)
+    if rc == -2:
+        return None
+    assert rc == 0, rc
+    return out
+
+
+def product_vnni(weights, k, x=None, threads=1, prepared=None):
+    """kapel-cpu's byte-activation product with its AVX-512 VNNI kernels
+    (bytes.rs:395-652); ``prepared`` = quantize_x(x) to skip that step.  None
+    where this host or a format does not take them."""
+    q, s, sums = prepared if prepared is not None else quantize_x(np.asarray(x, np.float32).reshape(-1, k))
+    count, fmts, groups, datas, ptrs, ns = _weights(weights)
+    out = np.zeros((q.shape[0], int(ns.sum())), dtype=np.float32)
+    rc = lib().ko_vnni_product_bytes(count, _p(fmts), _p(groups), _p(ptrs), _p(ns), k, _p(q), _p(s),
+                                     _p(sums), q.shape[0], _p(out), threads)
+    if rc == -2:
+        return None
     assert rc == 0, rc
     return out
 

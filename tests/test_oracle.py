@@ -721,3 +721,47 @@ def test_expert_product_in_bytes():
             e = xq[t] @ d.T
             bound = 1e-5 * (np.abs(xq[t]) @ np.abs(d).T) + 1e-6
             assert np.all(np.abs(got[t, j] - e) <= bound), (t, j)
+
+
+# ------------------------------------------- AVX-512 kernels (CPU baseline) ---
+
+WIDE, VNNI = ko.wide_available()
+
+
+@pytest.mark.skipif(not WIDE, reason="this host has no AVX-512")
+@pytest.mark.parametrize("fmt", ko.WIDE_FORMATS)
+def test_wide_products_match_the_dequantized_weights(fmt):
+    # quantized.rs:1150-1191 run on the AVX-512 kernels: 11 rows take the
+    # 8-, 2- and 1-row instances.
+    n, k, rows = 37, 1280, 11
+    i = np.arange(rows * k)
+    x = (((i * 7919) % 201).astype(np.float32) / np.float32(100.0) - np.float32(1.0)).reshape(rows, k)
+    w = lcg_blocks(fmt, 0, n * k // ko.block_len(fmt), 11)
+    e = x.astype(np.float64) @ ko.dequantize(fmt, 0, w).reshape(n, k).T
+    one = ko.product_wide([(fmt, 0, w, n)], k, x, threads=1)
+    assert np.all(np.abs(one - e) <= 1e-4 * (1 + np.abs(e)))
+    three = ko.product_wide([(fmt, 0, w, n)], k, x, threads=3)
+    assert np.array_equal(one.view(np.uint32), three.view(np.uint32))
+    # A dropped term or a wrong segment would be far from the portable kernel.
+    port = ko.product_f32([(fmt, 0, w, n)], k, x)
+    assert np.all(np.abs(one - port) <= 1e-4 * (1 + np.abs(port)))
+
+
+@pytest.mark.skipif(not VNNI, reason="this host has no AVX-512 VNNI")
+@pytest.mark.parametrize("fmt", ko.WIDE_FORMATS)
+@pytest.mark.parametrize("rows", [7, 6])
+def test_vnni_products_are_those_of_the_activations_in_bytes(fmt, rows):
+    # bytes.rs:720-774 on the VNNI kernels (views of 4 and 3, or 4 and 2 rows).
+    n, k = 13, 1024
+    x = byte_x(rows, k)
+    w = byte_blocks(fmt, 0, n * k // ko.block_len(fmt), 3)
+    dense = ko.dequantize(fmt, 0, w).reshape(n, k)
+    q, s, _ = ko.quantize_x(x)
+    xq = np.repeat(s.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+    e, size = xq @ dense.T, np.abs(xq) @ np.abs(dense).T
+    out = ko.product_vnni([(fmt, 0, w, n)], k, x, threads=3)
+    assert np.all(np.abs(out - e) <= 1e-5 * size + 1e-6)
+    port = ko.product_bytes([(fmt, 0, w, n)], k, x)
+    assert np.all(np.abs(out - port) <= 1e-5 * size + 1e-6)
+    again = ko.product_vnni([(fmt, 0, w, n)], k, x, threads=1)
+    assert np.array_equal(out.view(np.uint32), again.view(np.uint32))
