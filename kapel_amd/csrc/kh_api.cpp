@@ -10,6 +10,7 @@
 #include <algorithm>
 #include <cstdint>
 #include <cstdlib>
+#include <cstdio>
 #include <cstring>
 #include <vector>
 
@@ -218,9 +219,80 @@ Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     return p;
 }
 
+// The streamed decode kernel (gemv4_kernel): for one row of f32 activations
+// or up to four of bytes.  `tiles` tiles a workgroup and `ks` waves a tile
+// (contiguous ranges of units of K), as many workgroups as take at least one
+// round of the CUs with eight multiplying waves a workgroup; each wave's ring
+// holds its whole stream when that fits, else a multiple of both a copy (64
+// chunks) and a unit.
+struct Gemv4 {
+    bool ok = false;
+    int tiles, ks, npw, tb;
+    int init = 8;  // copies a wave issues before the activations' barrier
+};
+
+static int gcd_int(int a, int b) { return b ? gcd_int(b, a % b) : a; }
+
+Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, int tiles_total) {
+    Gemv4 p;
+    const int unit = gemv_unit(fmt, group);
+    const int len = (int)kh_block_len(fmt, group), bytes = (int)kh_block_bytes(fmt, group);
+    if (!unit || !len || k == 0) return p;
+    const int ub = (len >= unit ? 1 : unit / len) * bytes;
+    const int cw = (ub + (bytes % 4 ? 2 : 0) + 15) / 16;
+    const int uc = 16 * cw;
+    const int units = (int)div_up(k, unit);
+    const int quads = rows * units * unit / 4;
+    const size_t limit = 160 * 1024 - (fmt == KH_IQ3_S ? 2048 : 0);
+    // Preparing waves: one pass of loads over the activations where eight
+    // waves take them (256 quads a wave).
+    p.npw = std::max(1, std::min(8, (int)div_up(quads, 256)));
+    // One tile of eight waves a workgroup (two workgroups a CU).
+    const int T = 1;
+    int ks = std::min(units, 8);
+    const int step = 64 / gcd_int(64, uc) * uc / 64;  // copies of lcm(64, uc) chunks
+    for (; ks >= 1; ks--) {
+        if (p.npw + T * ks > 16) continue;
+        const int upw = (int)div_up(units, ks);
+        const size_t span = (size_t)units * unit;
+        size_t head = 16 + (size_t)rows * planes * span + span + (size_t)rows * (span / 32) * 16 +
+                      (size_t)T * ks * 16 * rows * 4;
+        head = (head + 15) / 16 * 16;
+        if (head >= limit) return p;
+        const int whole = (int)div_up((uint64_t)upw * uc, 64);
+        int tb = (int)((limit - head) / ((size_t)T * ks * 1024));
+        if (tb >= whole) tb = whole;
+        else tb = tb / step * step;
+        if (tb * 64 < 2 * uc + 64 && tb < whole) continue;
+        p.ok = true;
+        p.tiles = T;
+        p.ks = ks;
+        p.tb = tb;
+        return p;
+    }
+    return p;
+}
+
+// The decode kernel for one row of f32 activations (or up to four of
+// bytes): picked by the launch's size, or forced by KH_DECODE_KERNEL
+// ("staged": weights staged in LDS a workgroup at a time; "streamed":
+// streamed through per-wave rings; a test hook, read at each call).
+enum class DecodeKernel { AUTO, STAGED, STREAMED };
+DecodeKernel decode_kernel() {
+    const char *e = getenv("KH_DECODE_KERNEL");
+    if (!e) return DecodeKernel::AUTO;
+    if (!strcmp(e, "staged")) return DecodeKernel::STAGED;
+    if (!strcmp(e, "streamed")) return DecodeKernel::STREAMED;
+    return DecodeKernel::AUTO;
+}
+
 // The small-M kernel's bounded wait for its activations: 2^24 spins, or
 // KH_SPIN_LIMIT from the environment (a test hook: negative gives up at once,
 // which must leave NaN outputs, never wrong numbers).
+#ifdef KH_TRACE
+static int *g_trace = nullptr;
+extern "C" void kh_debug_trace(int *p) { g_trace = p; }
+#endif
 int spin_limit() {
     const char *e = getenv("KH_SPIN_LIMIT");
     return e ? atoi(e) : 1 << 24;
@@ -279,6 +351,7 @@ struct Launch {
     bool mm;          // the many-row product (rows r0 .. r0 + rows)
     GemvSplit gsplit;
     Gemv2 g2;         // the decode kernel staged in LDS, when it applies
+    Gemv4 g4;         // the streamed decode kernel, when it applies
     Split split;
     MmSplit msplit;
 };
@@ -321,6 +394,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
             L.rows = (int)std::min<uint64_t>(rows, gemv_max_rows(planes));
             L.gsplit = gemv_split(k, unit, L.tiles, L.rows, planes, (int)div_up(rows, L.rows), L.rows < (int)rows);
             L.g2 = Gemv2{};
+            L.g4 = Gemv4{};
             if (L.rows == (int)rows && (planes == 3 ? rows == 1 : rows <= 4)) {
                 // A workgroup's tiles in one matrix: several only when every
                 // matrix is a whole number of them.
@@ -328,6 +402,13 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
                 for (uint32_t m : L.members)
                     while (most > 1 && div_up(weights[m].n, 16) % most) most /= 2;
                 L.g2 = gemv2_plan(w.format, w.group, k, L.rows, planes, L.tiles, most);
+                // The streamed kernel where a launch takes several rounds of
+                // the CUs (measured: the 151936 x 4096 Q6_K table at M = 1
+                // 18 % shorter; launches of one round are as fast or faster
+                // staged), or where the caller asks for it.
+                const DecodeKernel dk = decode_kernel();
+                if (dk == DecodeKernel::STREAMED || (dk == DecodeKernel::AUTO && L.tiles >= 8 * cu_count()))
+                    L.g4 = gemv4_plan(w.format, w.group, k, L.rows, planes, L.tiles);
             }
             fn(L);
             continue;
@@ -463,6 +544,9 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
         if (L.gemv) {
             GemvArgs a{};
             a.spin_limit = spin_limit();
+#ifdef KH_TRACE
+            a.trace = g_trace;
+#endif
             a.count = (int)L.members.size();
             int tiles = 0;
             for (int m = 0; m < a.count; m++) {
@@ -511,7 +595,14 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.out = out;
             a.out_stride = c.width;
             a.width = c.width;
-            if (L.g2.ok) {
+            if (L.g4.ok) {
+                a.dma = 4;
+                a.tiles = L.g4.tiles;
+                a.npw = L.g4.npw;
+                a.kw = L.g4.ks;
+                a.tb = L.g4.tb;
+                a.chunk = L.g4.init;  // copies before the barrier
+            } else if (L.g2.ok) {
                 a.dma = 1;
                 a.tiles = L.g2.tiles;
                 a.npw = L.g2.npw;

@@ -533,6 +533,31 @@ struct Unit {
     __device__ static int local(int u) { return F::BLEN > F::U ? u % (F::BLEN / F::U) : 0; }
 };
 
+// A build with -DKH_TRACE (and kh_debug_trace(buffer) before a call) has
+// lane 0 of every wave of the decode kernels write s_memrealtime stamps (a
+// 100 MHz clock) at its phases: 32 ints a wave at (workgroup * 16 + wave) *
+// 32 -- start, loads issued or activations prepared, activations ready,
+// first data, multiplication done, end, HW_ID, XCC_ID, then (streamed
+// kernel) data ready and done for its first twelve units.  Off by default.
+#ifdef KH_TRACE
+#define KH_T(i)                                                                      \
+    do {                                                                              \
+        if (a.trace && lane == 0) {                                                   \
+            int *tr_ = a.trace + ((size_t)blockIdx.x * 16 + wave) * 32;                 \
+            tr_[i] = (int)__builtin_amdgcn_s_memrealtime();                           \
+            if (i == 0) {                                                             \
+                unsigned hw_, xcc_;                                                   \
+                asm volatile("s_getreg_b32 %0, hwreg(HW_REG_HW_ID)" : "=s"(hw_));     \
+                asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc_));   \
+                tr_[6] = (int)hw_;                                                    \
+                tr_[7] = (int)xcc_;                                                   \
+            }                                                                         \
+        }                                                                             \
+    } while (0)
+#else
+#define KH_T(i) do {} while (0)
+#endif
+
 template <class F, int P, int MT, int XK>
 __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
     using UN = Unit<F>;
@@ -552,6 +577,7 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
     const int g = lane >> 4, n16 = lane & 15;
     const int span = a.units * U;
     const int TB = a.tb;
+    KH_T(0);
 
     // LDS: planes [rows][P][span], zeros [span], info [rows][span / 32],
     // sums [kw][tiles][16][rows], weights [kw][TB KiB].
@@ -581,8 +607,11 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
             x_load<XK>(xin, 0, span, q0, threadIdx.x, 64 * a.npw, xv);
             x_prepare<P, XK>(xin, span, q0, threadIdx.x, 64 * a.npw, xv, planes, info);
         }
+        KH_T(1);
         lds_barrier();  // the activations are ready
+        KH_T(2);
         lds_barrier();  // the sums are written
+        KH_T(3);
         for (int o = threadIdx.x; o < T * 16 * rows; o += 64 * a.npw) {
             const int t = o / (16 * rows), r = (o / rows) % 16, m = o % rows;
             int mat;
@@ -592,6 +621,7 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
             for (int c = 1; c < a.kw; c++) v = v + sums[((c * a.tiles + t) * 16 + r) * rows + m];
             store_out(a.out_kind, a.out, (uint64_t)m * a.out_stride + a.col0[mat] + (uint64_t)n, v);
         }
+        KH_T(5);
         return;
     }
 
@@ -619,7 +649,9 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
         const uint32_t at = (uint32_t)n * (uint32_t)a.row_bytes + UN::block(u) * F::BYTES;
         KH_LDS_LOAD(src.r, mine + i * 1024, 16, on ? (at & ~3u) + 16u * c : lanes::NONE);
     }
+    KH_T(1);
     lds_barrier();  // the activations are ready
+    KH_T(2);
 
     // The A operand of this lane: row i = lane % 16 of each MFMA is (plane
     // or activation row) j = i % 4 of lane group i / 4, in that lane group's
@@ -705,6 +737,7 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
         for (int t = 0; t < T; t++) {
             // This tile's copies are the first ceil((t + 1) tchunks / 64).
             wait_vm_n(TB - (((t + 1) * tchunks + 63) >> 6));
+            if (t == 0) KH_T(3);
             float acc[ACC], acc2[ACC];
 #pragma unroll
             for (int i = 0; i < ACC; i++) acc[i] = acc2[i] = 0.0f;
@@ -722,6 +755,7 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
         int t = 0;
         for (; t + 1 < T; t += 2) {
             wait_vm_n(TB - (((t + 2) * tchunks + 63) >> 6));
+            if (t == 0) KH_T(3);
             float acc[ACC], acc2[ACC];
 #pragma unroll
             for (int i = 0; i < ACC; i++) acc[i] = acc2[i] = 0.0f;
@@ -747,11 +781,35 @@ __global__ __launch_bounds__(1024) void gemv2_kernel(GemvArgs a) {
             finish(t, acc);
         }
     }
+    KH_T(4);
     wait_vm_n(0);
     lds_barrier();  // the sums are written
+    KH_T(5);
 }
 
+}  // namespace kh
+#include "kh_gemv4.h"
+namespace kh {
+
 namespace {
+
+template <class F, int P, int MT, int XK>
+hipError_t launch4(const GemvArgs &a, hipStream_t s, size_t lds) {
+    static OncePerDevice once;
+    hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&gemv4_kernel<F, P, MT, XK>),
+                                 160 * 1024 - grid_lds<F>());
+    if (e != hipSuccess) return e;
+    int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
+    if (a.kw == 1 && a.count == 1) {
+        // Each wave walks its tiles: as many workgroups as are resident at once.
+        const int waves = a.npw + a.tiles;
+        const int per_cu = std::max(1, std::min((int)((160 * 1024) / std::max<size_t>(lds, 1)), 32 / waves));
+        groups = std::min(groups, cu_count() * per_cu);
+    }
+    hipLaunchKernelGGL((gemv4_kernel<F, P, MT, XK>), dim3((unsigned)groups), dim3(64 * (a.npw + a.tiles * a.kw)),
+                       lds, s, a);
+    return hipGetLastError();
+}
 
 template <class F, int P, int MT, int XK>
 hipError_t launch2(const GemvArgs &a, hipStream_t s, size_t lds) {
@@ -767,6 +825,20 @@ hipError_t launch2(const GemvArgs &a, hipStream_t s, size_t lds) {
 template <class F, int P, int XK>
 hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
     int mt = P == 3 ? a.rows : (a.rows + 3) / 4;
+    if (a.dma == 4) {
+        // Host-side checks of what the kernel assumes: its waves, a ring
+        // that holds the whole stream or a multiple of a unit and a copy of
+        // at least two units.
+        constexpr int UC = 16 * Unit<F>::CW;
+        const int upw = (a.units + a.kw - 1) / a.kw;
+        const int whole = (upw * UC + 63) / 64;
+        const bool ring_ok = a.tb >= whole || ((a.tb * 64) % UC == 0 && a.tb * 64 >= 2 * UC + 64);
+        const size_t lds = gemv4_lds(a.rows, P, a.units, F::U, a.tiles, a.kw, a.tb);
+        if (a.npw < 1 || a.tiles < 1 || a.kw < 1 || a.npw + a.tiles * a.kw > 16 || a.tb < 1 || !ring_ok ||
+            lds > (size_t)(160 * 1024 - grid_lds<F>()) || mt > 1)
+            return hipErrorInvalidValue;
+        return launch4<F, P, 1, XK>(a, s, lds);
+    }
     if (a.dma) {
         if (a.tb * 64 < a.tiles * 16 * Unit<F>::CW * ((a.units + a.kw - 1) / a.kw) || a.npw + a.kw > 16)
             return hipErrorInvalidValue;

@@ -41,6 +41,13 @@ size_t gemv2_lds(int rows, int planes, int units, int unit, int tiles, int kw, i
     return (head + 15) / 16 * 16 + (size_t)kw * tb * 1024;
 }
 
+size_t gemv4_lds(int rows, int planes, int units, int unit, int tiles, int ks, int tb) {
+    size_t span = (size_t)units * unit;
+    size_t head = 16 + (size_t)rows * planes * span + span + (size_t)rows * (span / 32) * 16 +
+                  (size_t)tiles * ks * 16 * rows * 4;
+    return (head + 15) / 16 * 16 + (size_t)tiles * ks * tb * 1024;
+}
+
 hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s) {
     switch (fmt) {
     case KH_Q2K: case KH_Q3K: case KH_Q4K: case KH_Q5K: case KH_Q6K:

@@ -41,6 +41,20 @@ struct OncePerDevice {
     hipError_t err[MAX_DEVICES] = {};
 };
 
+// The current device's compute units (queried once per device).
+inline int cu_count() {
+    static OncePerDevice once;
+    static int cus[MAX_DEVICES];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return 256;
+    std::call_once(once.flag[dev], [&] {
+        int n = 0;
+        once.err[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+        cus[dev] = once.err[dev] == hipSuccess && n > 0 ? n : 256;
+    });
+    return cus[dev];
+}
+
 inline hipError_t set_lds_limit(OncePerDevice &once, const void *kernel, int bytes) {
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
@@ -147,6 +161,9 @@ struct GemvArgs {
     // (its outputs then NaN): 2^24; negative (a test of the path only):
     // give up at once.
     int spin_limit;
+#ifdef KH_TRACE
+    int *trace;
+#endif
 };
 
 // The many-row product (kh_mm.h): weights of one format in column groups of
@@ -217,6 +234,7 @@ size_t gemv_lds(int rows, int planes, int chunk, int unit, int waves);
 hipError_t launch_gemv(uint32_t fmt, uint32_t group, int planes, const GemvArgs &a, hipStream_t s);
 // LDS bytes of a workgroup of the decode kernel staged in LDS.
 size_t gemv2_lds(int rows, int planes, int units, int unit, int tiles, int kw, int tb);
+size_t gemv4_lds(int rows, int planes, int units, int unit, int tiles, int ks, int tb);
 // The many-row product: the size of a format's scale groups (32 or 16; 0:
 // not read by it).
 int mm_group(uint32_t fmt, uint32_t group);

@@ -291,6 +291,7 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(...) emu::mfma32_f32x2(__VA_ARGS__)
 #define __builtin_amdgcn_sched_barrier(m) ((void)0)
 #define KH_PIN(x) ((void)0)
+#define KH_EMU_LDS 1
 #define KH_LDS_READ128(dst, ptr) memcpy(&(dst), (const void *)(ptr), 16)
 #define KH_LDS_LOAD(rsrc, lds, size, voff) emu::lds_load((rsrc), (void *)(lds), (size), (uint32_t)(voff))
 #define __builtin_amdgcn_s_waitcnt(n) ((void)0)
@@ -325,6 +326,13 @@ inline hipError_t hipGetSymbolAddress(void **p, T &symbol) {
 }
 inline hipError_t hipGetDevice(int *dev) {
     *dev = 0;
+    return hipSuccess;
+}
+// A small device: few compute units, so that the emulated launches that
+// size their grids by them walk several tiles a workgroup.
+enum hipDeviceAttribute_t { hipDeviceAttributeMultiprocessorCount = 1 };
+inline hipError_t hipDeviceGetAttribute(int *v, hipDeviceAttribute_t, int) {
+    *v = 2;
     return hipSuccess;
 }
 struct hipFuncAttributes {

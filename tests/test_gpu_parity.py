@@ -104,6 +104,66 @@ def test_products_of_every_format(hip, fmt, group):
         assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
 
 
+@pytest.fixture
+def streamed():
+    """The streamed decode kernel for every M = 1 launch it can take
+    (KH_DECODE_KERNEL is read at each call), then the automatic choice."""
+    os.environ["KH_DECODE_KERNEL"] = "streamed"
+    yield
+    os.environ.pop("KH_DECODE_KERNEL", None)
+
+
+@pytest.mark.parametrize("fmt,group", FORMATS)
+def test_streamed_decode_of_every_format(hip, streamed, fmt, group):
+    """The streamed decode kernel (per-wave rings) against f64 and against
+    the staged kernel: K of 19 blocks of 256 (odd blocks: rows that start 2
+    bytes past a dword for Q6_K and the other odd-sized blocks), K long
+    enough that a wave's ring wraps (16384), and a stack of three matrices
+    whose rows are not a whole number of tiles."""
+    cases = [(37, 4864), (24, 16384)]
+    for n, k in cases:
+        if k % ko.block_len(fmt, group):
+            continue
+        data, w = weight(fmt, group, n, k, 70 + fmt + n, hip)
+        x = x_uniform(1, k, n)
+        e64 = ko.product_f64([(fmt, group, data, n)], k, x)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        check_f32(got, e64, f"streamed fmt {fmt}/{group} n {n} k {k}")
+        again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        os.environ["KH_DECODE_KERNEL"] = "staged"
+        staged = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        os.environ["KH_DECODE_KERNEL"] = "streamed"
+        assert np.all(np.abs(got - staged) <= 2e-4 * (1 + np.abs(e64)))
+    k = 2048
+    if k % ko.block_len(fmt, group) == 0:
+        parts, ws = [], []
+        for i, n in enumerate((21, 5, 40)):
+            data, w = weight(fmt, group, n, k, 90 + i, hip)
+            parts.append((fmt, group, data, n))
+            ws.append(w)
+        x = x_uniform(1, k, 3)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x)] + ws).cpu().numpy()
+        check_f32(got, ko.product_f64(parts, k, x), f"streamed stack fmt {fmt}/{group}")
+
+
+def test_streamed_decode_with_byte_activations(hip, streamed):
+    """The streamed kernel with byte activations (up to four rows) is the
+    product of the quantized activations (bytes.rs:753-770)."""
+    k = 4096
+    for fmt, n in ((ka.Q4K, 40), (ka.Q6K, 33), (ka.Q8_0, 20)):
+        data, w = weight(fmt, 0, n, k, 11 + fmt, hip)
+        for rows in (1, 3, 4):
+            x = byte_x(rows, k)
+            q, s_, _ = ko.quantize_x(x)
+            xq = np.repeat(s_.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+            dense = ko.dequantize(fmt, 0, data).reshape(n, k)
+            e, size = xq @ dense.T, np.abs(xq) @ np.abs(dense).T
+            got = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+            hip.with_byte_activations(False)
+            assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6), (fmt, rows)
+
+
 def test_stacked_weights_of_several_formats(hip):
     """conformity.rs:936-947: [q4_k 5; q6_k 3; q8_0 2] x 512, one output."""
     k = 512
