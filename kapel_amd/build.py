@@ -45,6 +45,11 @@ def build(verbose=False):
         ("kh_mm_b.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_mm_i.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
         ("kh_mm_q.hip", HIPCC, HIP_FLAGS + MM_FLAGS),
+        ("kh_mmf.hip", HIPCC, HIP_FLAGS),
+        ("kh_mmf_k.hip", HIPCC, HIP_FLAGS),
+        ("kh_mmf_b.hip", HIPCC, HIP_FLAGS),
+        ("kh_mmf_i.hip", HIPCC, HIP_FLAGS),
+        ("kh_mmf_q.hip", HIPCC, HIP_FLAGS),
         ("kh_api.cpp", HIPCC, HIP_FLAGS),
         ("kh_quantize.cpp", "g++", HOST_FLAGS),
     )

@@ -286,6 +286,46 @@ DecodeKernel decode_kernel() {
     return DecodeKernel::AUTO;
 }
 
+// The many-row product of float activations: the bf16 matrix cores on
+// weights decoded in registers (mmf_kernel), or int8 MFMAs on three
+// fixed-point planes of the activations (mm_kernel).  Picked by the row
+// count, or forced by KH_MANY_KERNEL ("float", "int8"; a test hook read at
+// each call).
+constexpr uint64_t MMF_ROWS = 17;
+bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes) {
+    if (planes != 3 || !mm_group(fmt, group)) return false;
+    const char *e = getenv("KH_MANY_KERNEL");
+    if (e && !strcmp(e, "int8")) return false;
+    if (e && !strcmp(e, "float")) return true;
+    return rows >= MMF_ROWS;
+}
+
+// The split of an mmf launch: column groups of the kernel's weight rows, row
+// tiles of 128, K split as mm_split does.
+MmSplit mmf_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std::vector<uint32_t> &members) {
+    const kh_weight &w = weights[members[0]];
+    MmSplit m{};
+    launch_mmf(w.format, w.group, 1, MmArgs{}, nullptr, &m.cols);
+    m.mtiles = (int)div_up(rows, 128);
+    m.ngroups = 0;
+    for (uint32_t i : members) m.ngroups += (int)div_up(weights[i].n, m.cols);
+    const int unit = mm_unit(w.format, w.group);
+    m.units = (int)div_up(k, unit);
+    uint64_t base = (uint64_t)m.mtiles * m.ngroups;
+    int most = std::max(1, m.units / (int)div_up(512, unit));
+    auto cost = [&](int ks) { return div_up(base * ks, 256) * div_up(m.units, ks); };
+    int ks = 1;
+    uint64_t best = cost(1);
+    for (int s = 2; s <= most; s++)
+        if (cost(s) * 100 < best * 85) {
+            ks = s;
+            best = cost(s);
+        }
+    m.ups = (int)div_up(m.units, ks);
+    m.ks = (int)div_up(m.units, m.ups);
+    return m;
+}
+
 // The small-M kernel's bounded wait for its activations: 2^24 spins, or
 // KH_SPIN_LIMIT from the environment (a test hook: negative gives up at once,
 // which must leave NaN outputs, never wrong numbers).
@@ -303,10 +343,11 @@ int spin_limit() {
 struct Layout {
     uint64_t kpad;
     uint64_t counters_off, planes_off, xscale_off, xsum32_off, xsum16_off, xsumi16_off, xcopy_off;
+    uint64_t fplanes_off;  // bf16 planes of the float many-row product
     uint64_t partials_off, total;
 };
 
-Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats) {
+Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats, bool mmf) {
     Layout l{};
     l.kpad = align_up(std::max<uint64_t>(k, 64), 64);
     uint64_t at = 0;
@@ -326,6 +367,9 @@ Layout layout(uint64_t rows, uint64_t k, int planes, uint64_t partial_floats) {
     // vector loads.
     l.xcopy_off = at;
     if (rows <= 16) at = align_up(at + rows * k * 4, 256);
+    // Three bf16 planes a row (the most the float many-row product takes).
+    l.fplanes_off = at;
+    if (mmf) at = align_up(at + rows * 3 * l.kpad * 2, 256);
     l.partials_off = at;
     // Partial sums of the largest launch: segments x rows x columns.
     at = align_up(at + partial_floats * 4, 256);
@@ -337,6 +381,7 @@ struct Checked {
     uint64_t width = 0, max_wgs = 0, partial_floats = 0;
     bool bytes = false;
     bool any_qmv = false;  // a launch of the many-row product (prepared activations)
+    bool any_mmf = false;  // a launch of the float many-row product (bf16 planes)
     bool gemv_prep = false;  // a small-M launch in row chunks (prepared activations)
 };
 
@@ -349,6 +394,7 @@ struct Launch {
     int rows;
     bool gemv;        // the small-M product (all rows in one launch)
     bool mm;          // the many-row product (rows r0 .. r0 + rows)
+    bool mmf;         // ... of float activations on the bf16 matrix cores
     GemvSplit gsplit;
     Gemv2 g2;         // the decode kernel staged in LDS, when it applies
     Gemv4 g4;         // the streamed decode kernel, when it applies
@@ -385,6 +431,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         bool offsets32 = true;
         for (uint32_t m : L.members) offsets32 = offsets32 && weights[m].bytes < (1ull << 31);
         L.mm = false;
+        L.mmf = false;
         // Up to four rows the small-M product; from five the many-row
         // product is faster (measured across formats and shapes).
         bool one_chunk = rows <= (uint64_t)std::min(GEMV_DIRECT_ROWS, gemv_max_rows(planes));
@@ -417,12 +464,15 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         if (unit && offsets32 && mm_group(w.format, w.group)) {
             // Launches of at most 2 GiB of prepared activations each.
             L.mm = true;
+            L.mmf = use_mmf(w.format, w.group, rows, planes);
             uint64_t kpad = align_up(std::max<uint64_t>(k, 64), 64);
-            uint64_t fit = ((1ull << 31) - 1) / ((uint64_t)planes * kpad) / 64 * 64;
+            uint64_t fit = L.mmf ? ((1ull << 31) - 1) / (6 * kpad) / 128 * 128
+                                 : ((1ull << 31) - 1) / ((uint64_t)planes * kpad) / 64 * 64;
             for (uint64_t r0 = 0; r0 < rows; r0 += fit) {
                 L.r0 = r0;
                 L.rows = (int)std::min<uint64_t>(fit, rows - r0);
-                L.msplit = mm_split((uint64_t)L.rows, k, weights, L.members, planes);
+                L.msplit = L.mmf ? mmf_split((uint64_t)L.rows, k, weights, L.members)
+                                 : mm_split((uint64_t)L.rows, k, weights, L.members, planes);
                 fn(L);
             }
             continue;
@@ -475,7 +525,8 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
                 c.gemv_prep = c.gemv_prep || L.rows < (int)rows;
                 return;
             }
-            c.any_qmv = true;
+            if (L.mmf) c.any_mmf = true;
+            else c.any_qmv = true;
             if (L.mm) {
                 if (L.msplit.ks > 1)
                     c.partial_floats = std::max<uint64_t>(c.partial_floats,
@@ -510,6 +561,20 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
         p.xsum16 = reinterpret_cast<float *>(ws + l.xsum16_off);
         p.xsumi16 = reinterpret_cast<int32_t *>(ws + l.xsumi16_off);
         if ((err = launch_prep(p, s)) != hipSuccess) return err;
+    }
+    // bf16 planes, once for all weights: bf16 rows as they are, f16 rows in
+    // two planes, f32 rows in three.
+    const int fplanes = x_kind == KH_BF16 ? 1 : x_kind == KH_F16 ? 2 : 3;
+    if (c.any_mmf && !reuse) {
+        PrepBf16Args p{};
+        p.x_kind = x_kind;
+        p.x = x;
+        p.rows = rows;
+        p.k = k;
+        p.kpad = l.kpad;
+        p.planes = fplanes;
+        p.out = reinterpret_cast<uint16_t *>(ws + l.fplanes_off);
+        if ((err = launch_prep_bf16(p, s)) != hipSuccess) return err;
     }
     // Column of each weight.
     std::vector<uint64_t> col0(count);
@@ -638,6 +703,19 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.wmg = L.msplit.wmg;
             a.rows = L.rows;
             const uint64_t r0 = L.r0;
+            a.out_kind = out_kind;
+            a.out = static_cast<uint8_t *>(out) + r0 * c.width * kind_bytes(out_kind);
+            a.out_stride = c.width;
+            a.width = c.width;
+            a.partials = reinterpret_cast<float *>(ws + l.partials_off);
+            if (L.mmf) {
+                a.planes = reinterpret_cast<const int8_t *>(ws + l.fplanes_off) + r0 * fplanes * l.kpad * 2;
+                a.planes_bytes = (uint32_t)((uint64_t)L.rows * fplanes * l.kpad * 2);
+                a.kpad = l.kpad;
+                err = launch_mmf(w.format, w.group, fplanes, a, s, nullptr);
+                if (err == hipSuccess && a.ks > 1) err = launch_mm_reduce(a, s);
+                return;
+            }
             a.planes = reinterpret_cast<const int8_t *>(ws + l.planes_off) + r0 * planes * l.kpad;
             a.planes_bytes = (uint32_t)((uint64_t)L.rows * planes * l.kpad);
             a.kpad = l.kpad;
@@ -646,11 +724,6 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
                              : reinterpret_cast<const float *>(ws + l.xsum32_off) + r0 * (k / 32);
             a.hi = 65536.0f;
             a.shift = 8;
-            a.out_kind = out_kind;
-            a.out = static_cast<uint8_t *>(out) + r0 * c.width * kind_bytes(out_kind);
-            a.out_stride = c.width;
-            a.width = c.width;
-            a.partials = reinterpret_cast<float *>(ws + l.partials_off);
             err = launch_mm(w.format, w.group, planes, a, s);
             if (err == hipSuccess && a.ks > 1) err = launch_mm_reduce(a, s);
             return;
@@ -750,7 +823,7 @@ uint64_t kh_qmatmul_workspace(const kh_weight *weights, uint32_t count, uint64_t
                               uint32_t flags) {
     Checked c;
     if (check(weights, count, k, rows, flags, c) != KH_OK) return 0;
-    return layout(rows, k, c.bytes ? 1 : 3, c.partial_floats).total;
+    return layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.any_mmf).total;
 }
 
 int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_kind,
@@ -771,7 +844,7 @@ int kh_qmatmul(const kh_weight *weights, uint32_t count, uint64_t k, uint32_t x_
                    : KH_ERR_HIP;
     }
     if (!x) return KH_ERR_NULL;
-    Layout l = layout(rows, k, c.bytes ? 1 : 3, c.partial_floats);
+    Layout l = layout(rows, k, c.bytes ? 1 : 3, c.partial_floats, c.any_mmf);
     if (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255u))
         return KH_ERR_WORKSPACE;
     hipError_t err = plan_and_launch(weights, count, k, x_kind, x, rows, out_kind, out, c,
@@ -863,7 +936,7 @@ int kh_block_dots(const kh_weight *weight, uint64_t k, const int8_t *q, uint64_t
     if (!c.bytes) return KH_ERR_DTYPE;
     if (rows == 0 || weight->n == 0 || k == 0) return KH_OK;
     if (!q || !dots) return KH_ERR_NULL;
-    Layout l = layout(rows, k, 1, c.partial_floats);
+    Layout l = layout(rows, k, 1, c.partial_floats, false);
     if (!workspace || workspace_bytes < l.total || ((uintptr_t)workspace & 255u))
         return KH_ERR_WORKSPACE;
     uint8_t *ws = static_cast<uint8_t *>(workspace);

@@ -221,6 +221,20 @@ struct DequantArgs {
 };
 
 hipError_t launch_prep(const PrepArgs &a, hipStream_t s);
+
+// Activations as bf16 planes for the float many-row product (mmf_kernel):
+// [rows][planes][kpad] bf16: 1 plane (bf16 rows), 2 (f16) or 3 (f32).
+struct PrepBf16Args {
+    uint32_t x_kind;
+    const void *x;        // [rows, k]
+    uint64_t rows, k, kpad;
+    int planes;
+    uint16_t *out;
+};
+hipError_t launch_prep_bf16(const PrepBf16Args &a, hipStream_t s);
+// The float many-row product (bf16 planes in MmArgs::planes): one launch, or
+// with cols the weight rows of one of its column groups.
+hipError_t launch_mmf(uint32_t fmt, uint32_t group, int planes, const MmArgs &a, hipStream_t s, int *cols);
 hipError_t launch_fill(uint32_t *p, uint64_t words, hipStream_t s);
 hipError_t launch_fill_bytes(uint8_t *p, uint64_t bytes, hipStream_t s);
 hipError_t launch_qmv(uint32_t fmt, uint32_t group, int planes, const QmvArgs &a, dim3 grid,

@@ -98,6 +98,17 @@ __device__ __forceinline__ void rn(uint32_t (&w)[(R + 3) / 4], const Lds &s, uin
     for (int i = 0; i < W; i++) w[i] = __builtin_amdgcn_alignbyte(v[i + 1], v[i], a);
 }
 
+// The same reads straight from the weight matrix (buffer loads; offsets
+// past its end read zeros).
+template <int N>
+__device__ __forceinline__ void ld(uint32_t (&v)[N], const Src &s, uint32_t off) {
+    lanes::ldb<N>(v, s, off);
+}
+template <int R>
+__device__ __forceinline__ void rn(uint32_t (&w)[(R + 3) / 4], const Src &s, uint32_t off) {
+    lanes::run<R>(w, s, off);
+}
+
 // ------------------------------------------------ 256-element super-blocks
 // Q4_K: nibbles of sub-block 2c (low) and 2c + 1 (high) at 16 + 32c + l.
 struct Q4K {
@@ -106,7 +117,8 @@ struct Q4K {
     struct Regs {
         uint32_t h[4], q[4][4];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
         ld<4>(r.h, s, b);
 #pragma unroll
@@ -134,7 +146,8 @@ struct Q5K {
     struct Regs {
         uint32_t h[4], qh[4], q[4][4];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
         ld<4>(r.h, s, b);
         ld<4>(r.qh, s, b + 16 + 16 * h);
@@ -164,7 +177,8 @@ struct Q6K {
     struct Regs {
         uint32_t ql[8][2], qh[4][2], sc[5];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 8; i++)  // (a, t % 2, j % 2)
@@ -199,7 +213,8 @@ struct Q2K {
     struct Regs {
         uint32_t q[4][2], sc[4], dd[1];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 4; i++) ld<2>(r.q[i], s, b + 16 + 32 * (i >> 1) + 16 * (i & 1) + 8 * h);
@@ -230,7 +245,8 @@ struct Q3K {
     struct Regs {
         uint32_t hm[2][2], q[4][2], sc[4];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
 #pragma unroll
         for (int i = 0; i < 2; i++) rn<8>(r.hm[i], s, b + 16 * i + 8 * h);
@@ -272,7 +288,8 @@ struct Q8_0 {
     struct Regs {
         uint32_t c[4][4], d[4][1];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t b = row + (4 * u + j) * BYTES;
@@ -306,7 +323,8 @@ struct Q4_0 {
     struct Regs {
         uint32_t w[4][5];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) rn<18>(r.w[j], s, row + (4 * u + j) * BYTES);
     }
@@ -329,7 +347,8 @@ struct Q4_1 {
     struct Regs {
         uint32_t w[4][5];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) ld<5>(r.w[j], s, row + (4 * u + j) * BYTES);
     }
@@ -352,7 +371,8 @@ struct Q5x {
     struct Regs {
         uint32_t w[4][6];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             const uint32_t b = row + (4 * u + j) * BYTES;
@@ -400,7 +420,8 @@ struct Int8G {
     struct Regs {
         uint32_t c[NG][4], sc[NG][1];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
 #pragma unroll
         for (int j = 0; j < NG; j++) {
             const int p = NG * u + j;
@@ -425,7 +446,8 @@ struct Int4G {
     struct Regs {
         uint32_t c[NG][2], sc[NG][1];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
 #pragma unroll
         for (int j = 0; j < NG; j++) {
             const int p = NG * u + j;
@@ -467,7 +489,8 @@ struct IQ4NL {
     struct Regs {
         uint32_t w[4][5];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int) {
 #pragma unroll
         for (int j = 0; j < 4; j++) rn<18>(r.w[j], s, row + (4 * u + j) * BYTES);
     }
@@ -491,7 +514,8 @@ struct IQ4XS {
     struct Regs {
         uint32_t h[2], q[8][4];
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int) {
         const uint32_t b = row + u * BYTES;
         ld<2>(r.h, s, b);
 #pragma unroll
@@ -518,7 +542,8 @@ struct IQ3S {
     struct Regs {
         uint32_t c[8], hi[2], sg[8], sc, d;
     };
-    __device__ static void load(Regs &r, const Lds &s, uint32_t row, int u, int h) {
+    template <class S>
+    __device__ static void load(Regs &r, const S &s, uint32_t row, int u, int h) {
         const uint32_t b = row + u * BYTES;
         uint32_t t[1];
 #pragma unroll

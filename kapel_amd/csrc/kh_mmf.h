@@ -1,0 +1,324 @@
+// The product by quantized weights for many rows of float activations (f32,
+// bf16 or f16) on gfx950's bf16 matrix cores.
+//
+// Each weight is decoded in registers to its f32 value, scale * code -
+// minimum (the CPU decoders' value, kapel-cpu/src/quantized.rs:403-682), and
+// split into three bf16 parts w0 + w1 + w2: the top 16 bits of the f32, the
+// top 16 bits of what is left, and the rest rounded to bf16 (the weight to
+// 2^-24 of its size, as its f32).  The activations come as P bf16 planes x0 +
+// .. (prep_bf16_kernel), exactly: bf16 rows as they are (P = 1), f16 rows in
+// two planes, f32 rows in three.  Then
+//
+//     y[m, n] = sum_k x[m, k] w[n, k] ~= sum_k sum_{i + j <= 2} x_i w_j
+//
+// in f32 MFMAs (v_mfma_f32_32x32x16_bf16) over all of K (3, 5 or 6 MFMAs a
+// tile and 16 elements for P = 1, 2, 3; the terms left out are below 2^-24
+// of the product): the weights' scales and minimums are in their values, so
+// no work per scale group is left for the VALU.  This is the arithmetic of the
+// CPU's many-row path (rows decoded to f32, then an f32 product:
+// kapel-cpu/src/matmul.rs:198-239), each product to about f32's precision.
+// (Two parts a side, 16 bits, fail the CPU's tolerance 1e-4 (1 + |y|) where
+// large terms cancel.)
+//
+// A workgroup of four waves takes RM = 32 WM activation rows by 4 x 32 WN
+// weight rows; wave w the weight rows 32 WN w .. + 32 WN of the group, for
+// all RM activation rows (WM x WN tiles of 32 x 32).  Lane (c, h) supplies
+// row c of a tile and half h of each scale group: with groups of 32 the
+// codes 16h .. 16h + 15 (two MFMAs of 8), with groups of 16 the codes 8h ..
+// 8h + 7 (one MFMA).  The activations of an MFMA are the same 8 elements of
+// the activation row, so every MFMA adds exact bf16 products of matching
+// elements.
+//
+// K runs in steps of 64 elements.  The activations of a step ([P][RM][64]
+// bf16, 16-byte chunks swizzled by row) are loaded into registers two steps
+// ahead by every wave, written into one of two LDS slots one step ahead, and
+// read by all four waves; a wave's weight rows are loaded (buffer loads of
+// the lane readers of kh_mm.h) one unit ahead.  Every wait is the
+// compiler's: no direct-to-LDS copies.  Sums run in an order fixed by the
+// shapes (K in order within a workgroup, then the K splits in order by
+// mm_reduce_kernel).
+#pragma once
+#include "kh_mm.h"
+
+namespace kh {
+namespace mmf {
+
+using mm::v16f;
+using lanes::NONE;
+using lanes::Src;
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ v16f mfma(v4i a, v4i b, v16f c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+// Two f32 as packed bf16 (a low), rounded to nearest even.
+__device__ __forceinline__ uint32_t pk_bf16(float a, float b) {
+#ifdef KH_EMU_LDS
+    return (uint32_t)to_bf16(a) | ((uint32_t)to_bf16(b) << 16);
+#else
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f2{a, b}), b2));
+#endif
+}
+
+// NB codes (bytes, two's complement) of one scale group's lane part as
+// weights s * code + nm, split: part[j][NB / 2] packed bf16, element e in half
+// e % 2 of dword e / 2.  The code is taken as the unsigned byte of code + 128
+// (v_cvt_f32_ubyte), the 128 folded into the constant.
+template <int NB>
+__device__ __forceinline__ void split(const uint32_t (&q)[NB / 4], float s, float nm,
+                                      uint32_t (&part)[3][NB / 2]) {
+    const float c = fmaf(-128.0f, s, nm);
+    // An infinite or NaN weight keeps its first part and no others (w - w0
+    // would be NaN): every value of the group is finite or not with s and c.
+    const uint32_t keep = isfinite(s) && isfinite(c) ? 0xffffffffu : 0u;
+#pragma unroll
+    for (int d = 0; d < NB / 4; d++) {
+        const uint32_t u = q[d] ^ 0x80808080u;
+        float w[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) w[e] = fmaf(s, (float)((u >> (8 * e)) & 0xffu), c);
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const uint32_t b0 = __float_as_uint(w[2 * p]), b1 = __float_as_uint(w[2 * p + 1]);
+            const float r0 = w[2 * p] - __uint_as_float(b0 & 0xffff0000u);
+            const float r1 = w[2 * p + 1] - __uint_as_float(b1 & 0xffff0000u);
+            const uint32_t m0 = __float_as_uint(r0), m1 = __float_as_uint(r1);
+            part[0][2 * d + p] = __builtin_amdgcn_perm(b1, b0, 0x07060302u);
+            part[1][2 * d + p] = keep & __builtin_amdgcn_perm(m1, m0, 0x07060302u);
+            part[2][2 * d + p] = keep & pk_bf16(r0 - __uint_as_float(m0 & 0xffff0000u),
+                                                r1 - __uint_as_float(m1 & 0xffff0000u));
+        }
+    }
+}
+
+__device__ __forceinline__ void code_words(v4i c, uint32_t (&q)[4]) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) q[i] = (uint32_t)c[i];
+}
+__device__ __forceinline__ void code_words(uint64_t c, uint32_t (&q)[2]) {
+    q[0] = (uint32_t)c;
+    q[1] = (uint32_t)(c >> 32);
+}
+
+constexpr int WAVES = 4;
+
+template <class F, int P, int WM, int WN>
+struct Plan {
+    static constexpr int U = F::U, G = F::G, NG = F::NG, SPU = U / 64, GS = 64 / G;
+    static constexpr int RM = 32 * WM, NCOLS = WAVES * WN * 32;
+    static constexpr int XB = P * RM * 128;          // bytes of an activation slot
+    static constexpr int NXL = P * RM * 8 / (64 * WAVES);  // 16-byte loads a lane a step
+    static constexpr int LDS = 2 * XB;
+    static constexpr int NB = G / 2;                 // code bytes of a lane a group
+    static_assert(U % 64 == 0 && P * RM * 8 % (64 * WAVES) == 0, "whole steps and loads");
+};
+
+template <class F, int P, int WM, int WN>
+__global__ __launch_bounds__(256) void mmf_kernel(MmArgs a) {
+    using L = Plan<F, P, WM, WN>;
+    constexpr int U = F::U, G = F::G, NG = F::NG, SPU = L::SPU, GS = L::GS, RM = L::RM, NXL = L::NXL;
+    constexpr int NB = L::NB;
+    extern __shared__ __align__(16) uint8_t lds[];
+
+    // Workgroup -> (row tile, column group, K split), as mm_kernel.
+    const int b = blockIdx.x, local = b / XCDS;
+    const int mt = local % a.mtiles;
+    const int rest = (local / a.mtiles) * XCDS + b % XCDS;
+    if (rest >= a.ngroups * a.ks) return;
+    grid_fill<F>();
+    const int kz = rest / a.ngroups, ng = rest % a.ngroups;
+    const int u0 = kz * a.ups, u1 = min(a.units, u0 + a.ups);
+    const int m0 = mt * RM;
+
+    const int lane = threadIdx.x & 63, c = lane & 31, h = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wc = wave * WN * 32;
+    int mat = 0;
+    for (int i = 1; i < a.count; i++)
+        if (ng >= a.ng0[i]) mat = i;
+    const int64_t g0 = (int64_t)(ng - a.ng0[mat]) * L::NCOLS;
+    const int64_t nmat = (int64_t)a.n[mat];
+    const Src wsrc = lanes::source(a.w[mat], a.wbytes[mat]);
+    const Src xsrc = lanes::source(a.planes, a.planes_bytes);
+    uint32_t wrow[WN];
+#pragma unroll
+    for (int t = 0; t < WN; t++) {
+        const int64_t n = g0 + wc + t * 32 + c;
+        wrow[t] = n < nmat ? (uint32_t)n * (uint32_t)a.row_bytes : NONE;
+    }
+
+    // The activation chunks of a lane: chunk q = (i WAVES + wave) 64 + lane
+    // of a slot is plane p, row r, position q % 8 holding chunk (q % 8) ^ (r
+    // % 8) of the row's 128 bytes of the step.
+    const uint32_t kbytes = (uint32_t)a.kpad * 2u;
+    uint32_t xoff[NXL];
+#pragma unroll
+    for (int i = 0; i < NXL; i++) {
+        const int q = (i * WAVES + wave) * 64 + lane, pr = q / 8, r = pr % RM, p = pr / RM;
+        const int o = (q % 8) ^ (r & 7);
+        xoff[i] = m0 + r < a.rows ? (uint32_t)(((uint64_t)(m0 + r) * P + p) * kbytes) + 16u * o : NONE;
+    }
+    const int steps_end = (int)(a.kpad / 64);
+    auto load_x = [&](int step, v4i (&v)[NXL]) __attribute__((always_inline)) {
+        const bool on = step < steps_end && step < u1 * SPU;
+#pragma unroll
+        for (int i = 0; i < NXL; i++) {
+            const uint32_t off = on && xoff[i] != NONE ? xoff[i] + 128u * step : NONE;
+            v[i] = __builtin_bit_cast(v4i, __builtin_amdgcn_raw_buffer_load_b128(xsrc.r, (int)off, 0, 0));
+        }
+    };
+    auto store_x = [&](int slot, const v4i (&v)[NXL]) __attribute__((always_inline)) {
+        v4i *d = reinterpret_cast<v4i *>(lds + slot * L::XB);
+#pragma unroll
+        for (int i = 0; i < NXL; i++) d[(i * WAVES + wave) * 64 + lane] = v[i];
+    };
+    // The A operand of tile i, plane p, chunk o of the step (8 elements).
+    auto x_operand = [&](int slot, int i, int p, int o) __attribute__((always_inline)) {
+        const int r = i * 32 + c;
+        return *reinterpret_cast<const v4i *>(lds + slot * L::XB + ((p * RM + r) * 8 + (o ^ (r & 7))) * 16);
+    };
+
+    using Regs = typename F::Regs;
+    Regs Rn[WN], Rc[WN];
+    auto load_w = [&](int u) __attribute__((always_inline)) {
+#pragma unroll
+        for (int t = 0; t < WN; t++) F::load(Rn[t], wsrc, wrow[t], u, h);
+    };
+
+    v16f acc[WM][WN];
+#pragma unroll
+    for (int i = 0; i < WM; i++)
+#pragma unroll
+        for (int t = 0; t < WN; t++) acc[i][t] = v16f{};
+
+    // Prologue: step u0 SPU into slot 0; steps + 1 and + 2 in registers.
+    const int s0 = u0 * SPU;
+    v4i X[2][NXL];
+    load_w(u0);
+    load_x(s0, X[0]);
+    load_x(s0 + 1, X[1]);
+    store_x(0, X[0]);
+    load_x(s0 + 2, X[0]);
+
+    for (int u = u0; u < u1; u++) {
+#pragma unroll
+        for (int t = 0; t < WN; t++) Rc[t] = Rn[t];
+        if (u + 1 < u1) load_w(u + 1);
+        float sc[WN][NG], mn[WN][NG];
+#pragma unroll
+        for (int t = 0; t < WN; t++) {
+            F::scales(Rc[t], sc[t], mn[t]);
+#pragma unroll
+            for (int j = 0; j < NG; j++) {
+                if (!F::MIN) mn[t][j] = 0.0f;
+                if (U == 128 && u * U + j * G >= a.k) sc[t][j] = 0.0f, mn[t][j] = 0.0f;
+                mn[t][j] = -mn[t][j];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < SPU; i++) {
+            const int s = u * SPU + i;
+            // Slot s % 2 holds step s (written by every wave a step ago);
+            // every wave is done with slot (s + 1) % 2.  SPU is even, so i
+            // gives the slots and register sets.
+            // (The empty asms keep the compiler from moving LDS accesses
+            // across the barrier.)
+            __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+            store_x((i + 1) & 1, X[(i + 1) & 1]);
+            load_x(s + 3, X[(i + 1) & 1]);
+            const int slot = i & 1;
+#pragma unroll
+            for (int jj = 0; jj < GS; jj++) {
+                const int j = i * GS + jj;
+                uint32_t wp[WN][3][NB / 2];
+#pragma unroll
+                for (int t = 0; t < WN; t++) {
+                    uint32_t q[NB / 4];
+                    code_words(F::codes(Rc[t], j, h), q);
+                    split<NB>(q, sc[t][j], mn[t][j], wp[t]);
+                }
+#pragma unroll
+                for (int s2 = 0; s2 < NB / 8; s2++) {
+                    const int o = G == 32 ? 4 * jj + 2 * h + s2 : 2 * jj + h;
+#pragma unroll
+                    for (int mi = 0; mi < WM; mi++) {
+                        v4i xv[P];
+#pragma unroll
+                        for (int p = 0; p < P; p++) xv[p] = x_operand(slot, mi, p, o);
+#pragma unroll
+                        for (int t = 0; t < WN; t++) {
+                            v4i bw[3];
+#pragma unroll
+                            for (int j3 = 0; j3 < 3; j3++)
+                                bw[j3] = v4i{(int)wp[t][j3][4 * s2], (int)wp[t][j3][4 * s2 + 1],
+                                             (int)wp[t][j3][4 * s2 + 2], (int)wp[t][j3][4 * s2 + 3]};
+                            // x_i w_j for i + j <= 2, largest terms last.
+#pragma unroll
+                            for (int p = P - 1; p >= 0; p--)
+#pragma unroll
+                                for (int j3 = 2 - p; j3 >= 0; j3--) acc[mi][t] = mfma(xv[p], bw[j3], acc[mi][t]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+
+    // Lane (c, h), register v of tile (i, t): activation row i 32 + 8 (v / 4)
+    // + 4h + v % 4, weight row wc + 32 t + c.
+    const bool partial = a.ks > 1;
+#pragma unroll
+    for (int t = 0; t < WN; t++) {
+        const int64_t n = g0 + wc + t * 32 + c;
+        if (n >= nmat) continue;
+        const uint64_t col = a.col0[mat] + (uint64_t)n;
+#pragma unroll
+        for (int i = 0; i < WM; i++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int m = m0 + i * 32 + 8 * (v >> 2) + 4 * h + (v & 3);
+                if (m >= a.rows) continue;
+                if (partial) a.partials[((uint64_t)kz * a.rows + m) * a.width + col] = acc[i][t][v];
+                else store_out(a.out_kind, a.out, (uint64_t)m * a.out_stride + col, acc[i][t][v]);
+            }
+    }
+}
+
+template <class F, int P>
+hipError_t launch_p(const MmArgs &a, hipStream_t s) {
+    constexpr int WM = 4, WN = 2;
+    using L = Plan<F, P, WM, WN>;
+    constexpr int bytes = L::LDS;  // the IQ3_S grid is static LDS
+    static OncePerDevice once;
+    hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&mmf_kernel<F, P, WM, WN>), bytes);
+    if (e != hipSuccess) return e;
+    const int groups = a.ngroups * a.ks;
+    dim3 grid((unsigned)((groups + XCDS - 1) / XCDS * XCDS * a.mtiles)), block(64 * WAVES);
+    hipLaunchKernelGGL((mmf_kernel<F, P, WM, WN>), grid, block, (size_t)bytes, s, a);
+    return hipGetLastError();
+}
+
+// planes: 1 (bf16 activations), 2 (f16) or 3 (f32); cols: the weight rows of a column group
+// instead of a launch.
+template <class F>
+hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s, int *cols) {
+    if (cols) {
+        *cols = Plan<F, 1, 4, 2>::NCOLS;
+        return hipSuccess;
+    }
+    if (planes == 1) return launch_p<F, 1>(a, s);
+    if (planes == 2) return launch_p<F, 2>(a, s);
+    if (planes == 3) return launch_p<F, 3>(a, s);
+    return hipErrorInvalidValue;
+}
+
+}  // namespace mmf
+}  // namespace kh

@@ -12,7 +12,8 @@ OUT = os.path.join(HERE, "libkapel_hip_emu.so")
 CLANG = os.environ.get("EMU_CXX", "/opt/rocm/lib/llvm/bin/clang++")
 SOURCES = ["kh_kernels.hip", "kh_gemv.hip", "kh_gemv_k.hip", "kh_gemv_b.hip", "kh_gemv_i.hip",
            "kh_gemv_q.hip", "kh_mm_q.hip",
-           "kh_mm.hip", "kh_mm_k.hip", "kh_mm_b.hip", "kh_mm_i.hip", "kh_api.cpp", "kh_quantize.cpp"]
+           "kh_mm.hip", "kh_mm_k.hip", "kh_mm_b.hip", "kh_mm_i.hip", "kh_mmf.hip", "kh_mmf_k.hip",
+           "kh_mmf_b.hip", "kh_mmf_i.hip", "kh_mmf_q.hip", "kh_api.cpp", "kh_quantize.cpp"]
 FLAGS = ["-std=c++20", "-O1", "-g", "-fsanitize=address", "-fno-omit-frame-pointer", "-fPIC",
          "-ffp-contract=off", "-I", HERE, "-pthread", "-Wno-unused-command-line-argument"]
 

@@ -144,6 +144,35 @@ inline v16i mfma32_i8(const void *a, const void *b, v16i c) {
     return d;
 }
 inline v16i mfma32_i8x32(v4i a, v4i b, v16i c, int, int, int) { return mfma32_i8<16>(&a, &b, c); }
+
+// v_mfma_f32_32x32x16_bf16: 8 bf16 a lane, as the i8 MFMAs; the 16 exact
+// products summed in f64, rounded once, then added to C.
+inline v16f mfma32_bf16(v4i a, v4i b, v16f c) {
+    int w = wave_id(), l = lane_id();
+    std::memcpy(&block.slots[w][l][0], &a, 16);
+    std::memcpy(&block.slots[w][l][2], &b, 16);
+    wave_sync();
+    v16f d = c;
+    int j = l % 32;
+    for (int v = 0; v < 16; v++) {
+        int i = row32(l, v);
+        double sum = 0;
+        for (int half = 0; half < 2; half++) {
+            const uint16_t *ai = reinterpret_cast<const uint16_t *>(&block.slots[w][32 * half + i][0]);
+            const uint16_t *bj = reinterpret_cast<const uint16_t *>(&block.slots[w][32 * half + j][2]);
+            for (int k = 0; k < 8; k++) {
+                uint32_t x = (uint32_t)ai[k] << 16, y = (uint32_t)bj[k] << 16;
+                float fx, fy;
+                std::memcpy(&fx, &x, 4);
+                std::memcpy(&fy, &y, 4);
+                sum += (double)fx * (double)fy;
+            }
+        }
+        d[v] = c[v] + (float)sum;
+    }
+    wave_sync();
+    return d;
+}
 inline v16i mfma32_i8x16(long a, long b, v16i c, int, int, int) { return mfma32_i8<8>(&a, &b, c); }
 
 inline v16f mfma32_f32x2(float a, float b, v16f c, int, int, int) {
@@ -276,6 +305,9 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 namespace mm {
 alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 }
+namespace mmf {
+alignas(16) inline uint8_t lds[emu::LDS_BYTES];
+}
 }
 
 #define threadIdx (emu::self.tid)
@@ -289,6 +321,8 @@ alignas(16) inline uint8_t lds[emu::LDS_BYTES];
 #define __builtin_amdgcn_mfma_i32_32x32x32_i8(...) emu::mfma32_i8x32(__VA_ARGS__)
 #define __builtin_amdgcn_mfma_i32_32x32x16_i8(...) emu::mfma32_i8x16(__VA_ARGS__)
 #define __builtin_amdgcn_mfma_f32_32x32x2f32(...) emu::mfma32_f32x2(__VA_ARGS__)
+#define __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, x, y, z) \
+    emu::mfma32_bf16(__builtin_bit_cast(emu::v4i, (a)), __builtin_bit_cast(emu::v4i, (b)), (c))
 #define __builtin_amdgcn_sched_barrier(m) ((void)0)
 #define KH_PIN(x) ((void)0)
 #define KH_EMU_LDS 1

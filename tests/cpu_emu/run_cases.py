@@ -118,6 +118,35 @@ def case_product(fmt, group, n, k, rows, seed=5):
               ko.product_f64([(fmt, group, d, n)], k, x))
 
 
+def case_float_kinds(fmt, group, n, k, rows, kind, seed=7, kernel=None):
+    """The many-row product with bf16, f16 or f32 activations (f32 out),
+    against the f64 product of the activations as given; `kernel` forces the
+    float or the int8 many-row kernel (KH_MANY_KERNEL)."""
+    d = blocks(fmt, group, n * k // ko.block_len(fmt, group), seed + fmt)
+    x = xs(rows, k, 200 + rows)
+    if kind == BF16:
+        xb = (x.view(np.uint32) >> 16).astype(np.uint16)
+        x = (xb.astype(np.uint32) << 16).view(np.float32)
+    elif kind == F16:
+        xb = x.astype(np.float16).view(np.uint16)
+        x = xb.view(np.float16).astype(np.float32)
+    else:
+        xb = x
+    arr = (W * 1)(W(fmt, group, d.ctypes.data, d.size, n))
+    ws = workspace(L.kh_qmatmul_workspace(arr, 1, k, rows, 0))
+    out = np.full((rows, n), np.nan, np.float32)
+    if kernel:
+        os.environ["KH_MANY_KERNEL"] = kernel
+    try:
+        st = L.kh_qmatmul(arr, 1, k, kind, xb.ctypes.data, rows, F32, out.ctypes.data, 0,
+                          ws.ctypes.data, ws.size, None)
+    finally:
+        os.environ.pop("KH_MANY_KERNEL", None)
+    assert st == 0, st
+    check_f32(f"many rows fmt {fmt}/{group} n {n} k {k} rows {rows} kind {kind} {kernel or ''}", out,
+              ko.product_f64([(fmt, group, d, n)], k, x))
+
+
 def case_bytes(fmt, group, n, k, rows, dots=True):
     d = blocks(fmt, group, n * k // ko.block_len(fmt, group), 3)
     i = np.arange(rows * k)
@@ -293,6 +322,16 @@ def main(which):
     case_product(IQ3_S, 0, 300, 1024, 40)
     case_product(IQ4_XS, 0, 130, 512, 20)
     case_product(IQ4_NL, 0, 20, 96, 9)
+    # The float many-row kernel: bf16 / f16 / f32 activations (1, 2, 3
+    # planes), two row tiles, two column groups and a K split, groups of 16,
+    # a unit past K with minimums, Kapel's int4 groups; the int8 kernel it
+    # replaces, forced.
+    case_float_kinds(Q8_0, 0, 300, 1024, 140, BF16)
+    case_float_kinds(Q6K, 0, 70, 512, 20, F16)
+    case_float_kinds(Q4_1, 0, 40, 160, 30, F32)
+    case_float_kinds(INT4, 64, 40, 320, 25, BF16)
+    case_float_kinds(Q4K, 0, 300, 1024, 40, F32, kernel="int8")
+    case_float_kinds(Q8_0, 0, 20, 256, 5, F32, kernel="float")
     k = 512
     parts = [(Q4K, 0, blocks(Q4K, 0, n * k // 256, 60 + i), n) for i, n in enumerate((260, 7))]
     x = xs(21, k, 5)
