@@ -288,16 +288,18 @@ DecodeKernel decode_kernel() {
 
 // The many-row product of float activations: the bf16 matrix cores on
 // weights decoded in registers (mmf_kernel), or int8 MFMAs on three
-// fixed-point planes of the activations (mm_kernel).  Picked by the row
-// count, or forced by KH_MANY_KERNEL ("float", "int8"; a test hook read at
-// each call).
-constexpr uint64_t MMF_ROWS = 17;
-bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes) {
+// fixed-point planes of the activations (mm_kernel).  The first for bf16 and
+// f16 activations from 96 rows (measured, Q4_K / Q8_0 / Q6_K at 32 to 512
+// rows: 1.2-2.6x faster from 96 rows, slower below); f32 activations (three
+// bf16 planes, six MFMAs a product) are as fast or faster on the int8 planes.
+// KH_MANY_KERNEL ("float", "int8") forces one (a test hook read at each call).
+constexpr uint64_t MMF_ROWS = 96;
+bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x_kind) {
     if (planes != 3 || !mm_group(fmt, group)) return false;
     const char *e = getenv("KH_MANY_KERNEL");
     if (e && !strcmp(e, "int8")) return false;
     if (e && !strcmp(e, "float")) return true;
-    return rows >= MMF_ROWS;
+    return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= MMF_ROWS;
 }
 
 // The split of an mmf launch: column groups of the kernel's weight rows, row
@@ -406,7 +408,7 @@ struct Launch {
 // MAX_WEIGHTS at a time, by chunks of activation rows.
 template <class Fn>
 void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, int planes,
-                 Fn fn) {
+                 uint32_t x_kind, Fn fn) {
     std::vector<bool> done(count, false);
     for (uint32_t i = 0; i < count; i++) {
         if (done[i]) continue;
@@ -464,7 +466,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
         if (unit && offsets32 && mm_group(w.format, w.group)) {
             // Launches of at most 2 GiB of prepared activations each.
             L.mm = true;
-            L.mmf = use_mmf(w.format, w.group, rows, planes);
+            L.mmf = use_mmf(w.format, w.group, rows, planes, x_kind);
             uint64_t kpad = align_up(std::max<uint64_t>(k, 64), 64);
             uint64_t fit = L.mmf ? ((1ull << 31) - 1) / (6 * kpad) / 128 * 128
                                  : ((1ull << 31) - 1) / ((uint64_t)planes * kpad) / 64 * 64;
@@ -519,24 +521,27 @@ int check(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t rows, u
     c.bytes = byte_rows && all_bytes;
     c.max_wgs = div_up(tiles, 4) + count;
     if (c.max_wgs > MAX_COUNTERS) return KH_ERR_OVERFLOW;
+    // The workspace holds what the launches of any activation type need (the
+    // many-row kernel differs between bf16 / f16 and f32 rows).
     if (k > 0 && rows > 0)
-        each_launch(weights, count, k, rows, c.bytes ? 1 : 3, [&](const Launch &L) {
-            if (L.gemv) {
-                c.gemv_prep = c.gemv_prep || L.rows < (int)rows;
-                return;
-            }
-            if (L.mmf) c.any_mmf = true;
-            else c.any_qmv = true;
-            if (L.mm) {
-                if (L.msplit.ks > 1)
-                    c.partial_floats = std::max<uint64_t>(c.partial_floats,
-                                                          (uint64_t)L.msplit.ks * L.rows * c.width);
-                return;
-            }
-            if (L.split.segs > 1)
-                c.partial_floats = std::max<uint64_t>(
-                    c.partial_floats, (uint64_t)L.split.segs * L.rows * L.tiles * 16);
-        });
+        for (uint32_t kind : {(uint32_t)KH_F32, (uint32_t)KH_BF16})
+            each_launch(weights, count, k, rows, c.bytes ? 1 : 3, kind, [&](const Launch &L) {
+                if (L.gemv) {
+                    c.gemv_prep = c.gemv_prep || L.rows < (int)rows;
+                    return;
+                }
+                if (L.mmf) c.any_mmf = true;
+                else c.any_qmv = true;
+                if (L.mm) {
+                    if (L.msplit.ks > 1)
+                        c.partial_floats = std::max<uint64_t>(c.partial_floats,
+                                                              (uint64_t)L.msplit.ks * L.rows * c.width);
+                    return;
+                }
+                if (L.split.segs > 1)
+                    c.partial_floats = std::max<uint64_t>(
+                        c.partial_floats, (uint64_t)L.split.segs * L.rows * L.tiles * 16);
+            });
     return KH_OK;
 }
 
@@ -546,8 +551,15 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
                            hipStream_t s) {
     int planes = c.bytes ? 1 : 3;
     hipError_t err;
+    // What this call's launches read: int8 planes, bf16 planes.
+    bool need_qmv = false, need_mmf = false;
+    each_launch(weights, count, k, rows, planes, x_kind, [&](const Launch &L) {
+        if (L.gemv) return;
+        if (L.mmf) need_mmf = true;
+        else need_qmv = true;
+    });
     // The activations, once for all weights.
-    if ((c.any_qmv || c.gemv_prep) && !reuse) {
+    if ((need_qmv || c.gemv_prep) && !reuse) {
         PrepArgs p{};
         p.x_kind = x_kind;
         p.x = x;
@@ -565,7 +577,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     // bf16 planes, once for all weights: bf16 rows as they are, f16 rows in
     // two planes, f32 rows in three.
     const int fplanes = x_kind == KH_BF16 ? 1 : x_kind == KH_F16 ? 2 : 3;
-    if (c.any_mmf && !reuse) {
+    if (need_mmf && !reuse) {
         PrepBf16Args p{};
         p.x_kind = x_kind;
         p.x = x;
@@ -603,7 +615,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
         if ((err = launch_generic(g, s)) != hipSuccess) return err;
     }
     err = hipSuccess;
-    each_launch(weights, count, k, rows, planes, [&](const Launch &L) {
+    each_launch(weights, count, k, rows, planes, x_kind, [&](const Launch &L) {
         if (err != hipSuccess) return;
         const kh_weight &w = weights[L.members[0]];
         if (L.gemv) {

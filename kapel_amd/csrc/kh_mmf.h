@@ -118,8 +118,16 @@ struct Plan {
     static_assert(U % 64 == 0 && P * RM * 8 % (64 * WAVES) == 0, "whole steps and loads");
 };
 
+// Two workgroups a CU (two waves a SIMD, at most 256 registers each) for one
+// or two planes: one wave's waits for LDS, loads and barriers are the other's
+// MFMA time (measured: Q8_0 [gate; up] 24576 x 4096 at M = 512 with bf16
+// activations 415 us, against 479 us for one wave a SIMD with 256 rows a
+// workgroup); three planes take one.
+template <int P>
+constexpr int occupancy_of() { return P == 3 ? 1 : 2; }
+
 template <class F, int P, int WM, int WN>
-__global__ __launch_bounds__(256) void mmf_kernel(MmArgs a) {
+__global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
     using L = Plan<F, P, WM, WN>;
     constexpr int U = F::U, G = F::G, NG = F::NG, SPU = L::SPU, GS = L::GS, RM = L::RM, NXL = L::NXL;
     constexpr int NB = L::NB;
@@ -292,10 +300,20 @@ __global__ __launch_bounds__(256) void mmf_kernel(MmArgs a) {
     }
 }
 
+// Activation rows a workgroup takes: 256 for one or two planes, 128 for
+// three (registers); one weight tile a wave (128 weight rows a workgroup).
+// Activation rows a workgroup takes: 128 (four tiles a wave); one weight
+// tile a wave (128 weight rows a workgroup).
+template <int P>
+constexpr int wm_of() { return 4; }
+constexpr int WN_ALL = 1;
+
 template <class F, int P>
-hipError_t launch_p(const MmArgs &a, hipStream_t s) {
-    constexpr int WM = 4, WN = 2;
+hipError_t launch_p(const MmArgs &a_in, hipStream_t s) {
+    constexpr int WM = wm_of<P>(), WN = WN_ALL;
     using L = Plan<F, P, WM, WN>;
+    MmArgs a = a_in;
+    a.mtiles = (a.rows + L::RM - 1) / L::RM;
     constexpr int bytes = L::LDS;  // the IQ3_S grid is static LDS
     static OncePerDevice once;
     hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&mmf_kernel<F, P, WM, WN>), bytes);
@@ -311,7 +329,7 @@ hipError_t launch_p(const MmArgs &a, hipStream_t s) {
 template <class F>
 hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s, int *cols) {
     if (cols) {
-        *cols = Plan<F, 1, 4, 2>::NCOLS;
+        *cols = Plan<F, 1, wm_of<1>(), WN_ALL>::NCOLS;
         return hipSuccess;
     }
     if (planes == 1) return launch_p<F, 1>(a, s);

@@ -327,9 +327,10 @@ def main(which):
     # a unit past K with minimums, Kapel's int4 groups; the int8 kernel it
     # replaces, forced.
     case_float_kinds(Q8_0, 0, 300, 1024, 140, BF16)
-    case_float_kinds(Q6K, 0, 70, 512, 20, F16)
-    case_float_kinds(Q4_1, 0, 40, 160, 30, F32)
-    case_float_kinds(INT4, 64, 40, 320, 25, BF16)
+    case_float_kinds(Q6K, 0, 70, 512, 20, F16, kernel="float")
+    case_float_kinds(Q4_1, 0, 40, 160, 30, F32, kernel="float")
+    case_float_kinds(INT4, 64, 40, 320, 25, BF16, kernel="float")
+    case_float_kinds(IQ3_S, 0, 40, 512, 100, BF16)
     case_float_kinds(Q4K, 0, 300, 1024, 40, F32, kernel="int8")
     case_float_kinds(Q8_0, 0, 20, 256, 5, F32, kernel="float")
     k = 512

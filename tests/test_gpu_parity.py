@@ -524,6 +524,76 @@ def test_many_rows_of_every_format(hip, fmt, group):
             assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6), f"bytes fmt {fmt}/{group} rows {rows}"
 
 
+@pytest.fixture
+def float_kernel():
+    """The float many-row kernel forced at every row count (KH_MANY_KERNEL is
+    read at each call), then the automatic choice."""
+    os.environ["KH_MANY_KERNEL"] = "float"
+    yield
+    os.environ.pop("KH_MANY_KERNEL", None)
+
+
+MM_FORMATS = [f for f in FORMATS if f[0] not in (ka.INT8, ka.INT4) or f[1] in (32, 64, 128)]
+
+
+def product_f32_out(hip, xt, ws):
+    """kh_qmatmul with f32 outputs whatever the activations' type (the C ABI
+    takes the two types apart; the Python op gives x's type)."""
+    rows, k = xt.shape
+    arr = (ka._Weight * len(ws))(*[w.weight() for w in ws])
+    width = sum(w.n for w in ws)
+    space = hip.workspace(ka.lib().kh_qmatmul_workspace(arr, len(ws), k, rows, 0))
+    out = torch.full((rows, width), float("nan"), device="cuda:0")
+    st = ka.lib().kh_qmatmul(arr, len(ws), k, ka.float_kind(xt.dtype), xt.data_ptr(), rows, 0,
+                             out.data_ptr(), 0, space.data_ptr(), space.numel(), hip.stream())
+    assert st == 0, st
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("fmt,group", MM_FORMATS)
+def test_float_many_row_kernel_of_every_format(hip, float_kernel, fmt, group):
+    """The many-row product on the bf16 matrix cores (weights in three bf16
+    parts, activations in one, two or three exact bf16 planes): bf16, f16 and
+    f32 activations, 130 rows (a full and a partial row tile) by 300 weight
+    rows (partial column group) with K split, against the f64 product of the
+    activations as given within 1e-4 (1 + |e|) + 1e-7 sum|x w|, as the f32
+    many-row test; bitwise equal on a second run."""
+    k, n, rows = 1280, 300, 130
+    data, w = weight(fmt, group, n, k, 90 + fmt, hip)
+    dense = ko.dequantize(fmt, group, data).reshape(n, k)
+    x32 = x_uniform(rows, k, 500 + fmt)
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        xt = dev(x32, dtype)
+        x = xt.float().cpu().numpy().astype(np.float64)
+        got = product_f32_out(hip, xt, [w]).astype(np.float64)
+        e64 = x @ dense.T
+        size = np.abs(x) @ np.abs(dense).T
+        bad = np.abs(got - e64) > 1e-4 * (1 + np.abs(e64)) + 1e-7 * size
+        assert not bad.any(), f"fmt {fmt}/{group} {dtype}: {np.argwhere(bad)[:3]}"
+        again = product_f32_out(hip, xt, [w])
+        assert np.array_equal(got.astype(np.float32).view(np.uint32), again.view(np.uint32))
+
+
+def test_float_many_row_kernel_is_the_default_for_bf16_rows(hip):
+    """From 96 rows of bf16 activations the automatic choice is the float
+    kernel: its result equals the forced float kernel's bit for bit, and the
+    int8-plane kernel's within the f32 bar."""
+    k, n, rows = 512, 260, 96
+    data, w = weight(ka.Q4K, 0, n, k, 77, hip)
+    xt = dev(x_uniform(rows, k, 77), torch.bfloat16)
+    auto = product_f32_out(hip, xt, [w])
+    res = {}
+    for kern in ("float", "int8"):
+        os.environ["KH_MANY_KERNEL"] = kern
+        try:
+            res[kern] = product_f32_out(hip, xt, [w])
+        finally:
+            os.environ.pop("KH_MANY_KERNEL", None)
+    assert np.array_equal(auto.view(np.uint32), res["float"].view(np.uint32))
+    e = res["int8"].astype(np.float64)
+    assert np.all(np.abs(auto - e) <= 1e-4 * (1 + np.abs(e)))
+
+
 QWEN3_8B = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
             ("gate", 12288, 4096), ("up", 12288, 4096), ("down", 4096, 12288)]
 
