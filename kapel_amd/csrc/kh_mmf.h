@@ -228,6 +228,31 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
                 mn[t][j] = -mn[t][j];
             }
         }
+        // The unit's groups in order, software-pipelined: the weights of
+        // group j + 1 are decoded, and the activations of the next slot read,
+        // while the MFMAs of the current slot run.
+        constexpr int SPG = NB / 8;  // slots (16 elements of K) a group
+        uint32_t wcur[WN][3][NB / 2], wnxt[WN][3][NB / 2];
+        auto decode = [&](int j, uint32_t (&wp)[WN][3][NB / 2]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int t = 0; t < WN; t++) {
+                uint32_t q[NB / 4];
+                code_words(F::codes(Rc[t], j, h), q);
+                split<NB>(q, sc[t][j], mn[t][j], wp[t]);
+            }
+        };
+        auto read_x = [&](int slot, int o, v4i (&xv)[WM][P]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+                for (int p = 0; p < P; p++) xv[mi][p] = x_operand(slot, mi, p, o);
+        };
+        // Chunk of the step's 128 bytes holding slot z's 8 elements.
+        auto chunk = [&](int z) __attribute__((always_inline)) {
+            const int jj = z / SPG, s2 = z % SPG;
+            return G == 32 ? 4 * jj + 2 * h + s2 : 2 * jj + h;
+        };
+        decode(0, wcur);
 #pragma unroll
         for (int i = 0; i < SPU; i++) {
             const int s = u * SPU + i;
@@ -243,39 +268,40 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
             store_x((i + 1) & 1, X[(i + 1) & 1]);
             load_x(s + 3, X[(i + 1) & 1]);
             const int slot = i & 1;
+            v4i xc[WM][P], xn[WM][P];
+            read_x(slot, chunk(0), xc);
 #pragma unroll
-            for (int jj = 0; jj < GS; jj++) {
-                const int j = i * GS + jj;
-                uint32_t wp[WN][3][NB / 2];
+            for (int z = 0; z < 4; z++) {
+                const int jj = z / SPG, s2 = z % SPG, j = i * GS + jj;
+                if (z + 1 < 4) read_x(slot, chunk(z + 1), xn);
+                if (s2 == SPG - 1 && j + 1 < NG) decode(j + 1, wnxt);
 #pragma unroll
-                for (int t = 0; t < WN; t++) {
-                    uint32_t q[NB / 4];
-                    code_words(F::codes(Rc[t], j, h), q);
-                    split<NB>(q, sc[t][j], mn[t][j], wp[t]);
-                }
+                for (int mi = 0; mi < WM; mi++)
 #pragma unroll
-                for (int s2 = 0; s2 < NB / 8; s2++) {
-                    const int o = G == 32 ? 4 * jj + 2 * h + s2 : 2 * jj + h;
+                    for (int t = 0; t < WN; t++) {
+                        v4i bw[3];
 #pragma unroll
-                    for (int mi = 0; mi < WM; mi++) {
-                        v4i xv[P];
+                        for (int j3 = 0; j3 < 3; j3++)
+                            bw[j3] = v4i{(int)wcur[t][j3][4 * s2], (int)wcur[t][j3][4 * s2 + 1],
+                                         (int)wcur[t][j3][4 * s2 + 2], (int)wcur[t][j3][4 * s2 + 3]};
+                        // x_i w_j for i + j <= 2, largest terms last.
 #pragma unroll
-                        for (int p = 0; p < P; p++) xv[p] = x_operand(slot, mi, p, o);
+                        for (int p = P - 1; p >= 0; p--)
 #pragma unroll
-                        for (int t = 0; t < WN; t++) {
-                            v4i bw[3];
-#pragma unroll
-                            for (int j3 = 0; j3 < 3; j3++)
-                                bw[j3] = v4i{(int)wp[t][j3][4 * s2], (int)wp[t][j3][4 * s2 + 1],
-                                             (int)wp[t][j3][4 * s2 + 2], (int)wp[t][j3][4 * s2 + 3]};
-                            // x_i w_j for i + j <= 2, largest terms last.
-#pragma unroll
-                            for (int p = P - 1; p >= 0; p--)
-#pragma unroll
-                                for (int j3 = 2 - p; j3 >= 0; j3--) acc[mi][t] = mfma(xv[p], bw[j3], acc[mi][t]);
-                        }
+                            for (int j3 = 2 - p; j3 >= 0; j3--) acc[mi][t] = mfma(xc[mi][p], bw[j3], acc[mi][t]);
                     }
-                }
+                if (z + 1 < 4)
+#pragma unroll
+                    for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+                        for (int p = 0; p < P; p++) xc[mi][p] = xn[mi][p];
+                if (s2 == SPG - 1 && j + 1 < NG)
+#pragma unroll
+                    for (int t = 0; t < WN; t++)
+#pragma unroll
+                        for (int j3 = 0; j3 < 3; j3++)
+#pragma unroll
+                            for (int e = 0; e < NB / 2; e++) wcur[t][j3][e] = wnxt[t][j3][e];
             }
         }
     }
