@@ -368,8 +368,8 @@ def main():
             hip.with_byte_activations(False)
             ops4 = 2 * 512 * sum(n * k for _, n, k in QWEN_LAYER)
             # The reference's own arithmetic at 512 rows: activations as they
-            # are (the float many-row kernel: weights decoded to three bf16
-            # parts, bf16 activations in one plane, f32 MFMAs).
+            # are (the float many-row kernel: bf16 activations and the Q8_0
+            # codes on the bf16 matrix cores, f32 sums scaled by block).
             reserve(QWEN_CALLS, qlayers[0], 512, False)
             s4f, _ = timed([qwen_step(0), qwen_step(1)], 4, 2)
             configs["4"] = {"workload": "Qwen3-8B layer in Q8_0, M = 512, bf16 activations quantized to bytes",
@@ -379,8 +379,8 @@ def main():
                             "bf16_activations": {"ms_per_step": round(s4f * 1e3, 3),
                                                  "tops": round(ops4 / s4f / 1e12, 2),
                                                  "note": "activations not rounded to bytes (the drop-in "
-                                                         "default above 16 rows): bf16 matrix cores on weights "
-                                                         "decoded to three bf16 parts"}}
+                                                         "default above 16 rows): bf16 matrix cores, the Q8_0 "
+                                                         "codes as bf16 and one scale fma per block of 32"}}
             del qlayers
 
         if "moe" in only:

@@ -96,6 +96,19 @@ __device__ __forceinline__ void split(const uint32_t (&q)[NB / 4], float s, floa
     }
 }
 
+// NB signed codes as exact bf16 (|code| <= 128 has at most 8 significant
+// bits), packed as split() packs.
+template <int NB>
+__device__ __forceinline__ void codes_bf16(const uint32_t (&q)[NB / 4], uint32_t (&b)[NB / 2]) {
+#pragma unroll
+    for (int d = 0; d < NB / 4; d++)
+#pragma unroll
+        for (int p = 0; p < 2; p++) {
+            const float f0 = (float)(int8_t)(q[d] >> (16 * p)), f1 = (float)(int8_t)(q[d] >> (16 * p + 8));
+            b[2 * d + p] = __builtin_amdgcn_perm(__float_as_uint(f1), __float_as_uint(f0), 0x07060302u);
+        }
+}
+
 __device__ __forceinline__ void code_words(v4i c, uint32_t (&q)[4]) {
 #pragma unroll
     for (int i = 0; i < 4; i++) q[i] = (uint32_t)c[i];
@@ -106,6 +119,11 @@ __device__ __forceinline__ void code_words(uint64_t c, uint32_t (&q)[2]) {
 }
 
 constexpr int WAVES = 4;
+
+// The dot mode (codes as the B operand, one scale fma per output and group):
+// units of 128 elements without a minimum term.
+template <class F>
+constexpr bool dot_mode() { return !F::MIN && F::U == 128; }
 
 template <class F, int P, int WM, int WN>
 struct Plan {
@@ -119,15 +137,16 @@ struct Plan {
 };
 
 // Two workgroups a CU (two waves a SIMD, at most 256 registers each) for one
-// or two planes: one wave's waits for LDS, loads and barriers are the other's
-// MFMA time (measured: Q8_0 [gate; up] 24576 x 4096 at M = 512 with bf16
-// activations 415 us, against 479 us for one wave a SIMD with 256 rows a
-// workgroup); three planes take one.
-template <int P>
-constexpr int occupancy_of() { return P == 3 ? 1 : 2; }
+// plane, and for two in the dot mode: one wave's waits for LDS, loads and
+// barriers are the other's MFMA time (measured: Q8_0 [gate; up] 24576 x 4096
+// at M = 512 with bf16 activations 415 us, against 479 us for one wave a SIMD
+// with 256 rows a workgroup).  One workgroup a CU otherwise (the registers
+// of three planes, or of two with split weights, would spill).
+template <class F, int P>
+constexpr int occupancy_of() { return P == 1 || (P == 2 && dot_mode<F>()) ? 2 : 1; }
 
 template <class F, int P, int WM, int WN>
-__global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
+__global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs a) {
     using L = Plan<F, P, WM, WN>;
     constexpr int U = F::U, G = F::G, NG = F::NG, SPU = L::SPU, GS = L::GS, RM = L::RM, NXL = L::NXL;
     constexpr int NB = L::NB;
@@ -231,14 +250,26 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
         // The unit's groups in order, software-pipelined: the weights of
         // group j + 1 are decoded, and the activations of the next slot read,
         // while the MFMAs of the current slot run.
+        //
+        // Blocks of 32 without a minimum term (DOT): the codes themselves are the
+        // B operand (exact in bf16); each group's dot of codes and
+        // activations, sum_k q x (planes summed), is an f32 MFMA result, and
+        // joins the sums as acc += scale * dot (one fma per output and group).
+        // Other formats (a minimum term, or 256-element units whose scales
+        // and dot sums would not fit the registers of two waves a SIMD): the
+        // weights' values in three bf16 parts (split).
+        constexpr bool DOT = dot_mode<F>();
+        constexpr int WPARTS = DOT ? 1 : 3;
         constexpr int SPG = NB / 8;  // slots (16 elements of K) a group
-        uint32_t wcur[WN][3][NB / 2], wnxt[WN][3][NB / 2];
-        auto decode = [&](int j, uint32_t (&wp)[WN][3][NB / 2]) __attribute__((always_inline)) {
+        uint32_t wcur[WN][WPARTS][NB / 2], wnxt[WN][WPARTS][NB / 2];
+        v16f dot[DOT ? WM : 1][DOT ? WN : 1];
+        auto decode = [&](int j, uint32_t (&wp)[WN][WPARTS][NB / 2]) __attribute__((always_inline)) {
 #pragma unroll
             for (int t = 0; t < WN; t++) {
                 uint32_t q[NB / 4];
                 code_words(F::codes(Rc[t], j, h), q);
-                split<NB>(q, sc[t][j], mn[t][j], wp[t]);
+                if constexpr (DOT) codes_bf16<NB>(q, wp[t][0]);
+                else split<NB>(q, sc[t][j], mn[t][j], *reinterpret_cast<uint32_t(*)[3][NB / 2]>(wp[t]));
             }
         };
         auto read_x = [&](int slot, int o, v4i (&xv)[WM][P]) __attribute__((always_inline)) {
@@ -279,17 +310,34 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
                 for (int mi = 0; mi < WM; mi++)
 #pragma unroll
                     for (int t = 0; t < WN; t++) {
-                        v4i bw[3];
+                        v4i bw[WPARTS];
 #pragma unroll
-                        for (int j3 = 0; j3 < 3; j3++)
+                        for (int j3 = 0; j3 < WPARTS; j3++)
                             bw[j3] = v4i{(int)wcur[t][j3][4 * s2], (int)wcur[t][j3][4 * s2 + 1],
                                          (int)wcur[t][j3][4 * s2 + 2], (int)wcur[t][j3][4 * s2 + 3]};
-                        // x_i w_j for i + j <= 2, largest terms last.
+                        if constexpr (DOT) {
 #pragma unroll
-                        for (int p = P - 1; p >= 0; p--)
+                            for (int p = P - 1; p >= 0; p--)
+                                dot[mi][t] = mfma(xc[mi][p], bw[0], s2 == 0 && p == P - 1 ? v16f{} : dot[mi][t]);
+                        } else {
+                            // x_i w_j for i + j <= 2, largest terms last.
 #pragma unroll
-                            for (int j3 = 2 - p; j3 >= 0; j3--) acc[mi][t] = mfma(xc[mi][p], bw[j3], acc[mi][t]);
+                            for (int p = P - 1; p >= 0; p--)
+#pragma unroll
+                                for (int j3 = 2 - p; j3 >= 0; j3--)
+                                    acc[mi][t] = mfma(xc[mi][p], bw[j3], acc[mi][t]);
+                        }
                     }
+                if constexpr (DOT) {
+                    if (s2 == SPG - 1)
+#pragma unroll
+                        for (int mi = 0; mi < WM; mi++)
+#pragma unroll
+                            for (int t = 0; t < WN; t++)
+#pragma unroll
+                                for (int v = 0; v < 16; v++)
+                                    acc[mi][t][v] = fmaf(dot[mi][t][v], sc[t][j], acc[mi][t][v]);
+                }
                 if (z + 1 < 4)
 #pragma unroll
                     for (int mi = 0; mi < WM; mi++)
@@ -299,7 +347,7 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
 #pragma unroll
                     for (int t = 0; t < WN; t++)
 #pragma unroll
-                        for (int j3 = 0; j3 < 3; j3++)
+                        for (int j3 = 0; j3 < WPARTS; j3++)
 #pragma unroll
                             for (int e = 0; e < NB / 2; e++) wcur[t][j3][e] = wnxt[t][j3][e];
             }
@@ -328,15 +376,18 @@ __global__ __launch_bounds__(256, occupancy_of<P>()) void mmf_kernel(MmArgs a) {
 
 // Activation rows a workgroup takes: 256 for one or two planes, 128 for
 // three (registers); one weight tile a wave (128 weight rows a workgroup).
-// Activation rows a workgroup takes: 128 (four tiles a wave); one weight
-// tile a wave (128 weight rows a workgroup).
-template <int P>
-constexpr int wm_of() { return 4; }
+// Activation rows a workgroup takes: 128 (four tiles a wave) where the
+// weights are split into three parts, 64 (two tiles a wave) for the dot mode
+// (its dot sums take the registers of two more tiles; measured on the Q8_0
+// layer of config 4 at M = 512: 12 % shorter than four tiles a wave at one
+// wave a SIMD); one weight tile a wave (128 weight rows a workgroup).
+template <class F, int P>
+constexpr int wm_of() { return dot_mode<F>() ? 2 : 4; }
 constexpr int WN_ALL = 1;
 
 template <class F, int P>
 hipError_t launch_p(const MmArgs &a_in, hipStream_t s) {
-    constexpr int WM = wm_of<P>(), WN = WN_ALL;
+    constexpr int WM = wm_of<F, P>(), WN = WN_ALL;
     using L = Plan<F, P, WM, WN>;
     MmArgs a = a_in;
     a.mtiles = (a.rows + L::RM - 1) / L::RM;
@@ -355,7 +406,7 @@ hipError_t launch_p(const MmArgs &a_in, hipStream_t s) {
 template <class F>
 hipError_t launch_f(const MmArgs &a, int planes, hipStream_t s, int *cols) {
     if (cols) {
-        *cols = Plan<F, 1, wm_of<1>(), WN_ALL>::NCOLS;
+        *cols = Plan<F, 1, wm_of<F, 1>(), WN_ALL>::NCOLS;
         return hipSuccess;
     }
     if (planes == 1) return launch_p<F, 1>(a, s);
