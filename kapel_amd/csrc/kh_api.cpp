@@ -286,20 +286,29 @@ DecodeKernel decode_kernel() {
     return DecodeKernel::AUTO;
 }
 
-// The many-row product of float activations: the bf16 matrix cores on
-// weights decoded in registers (mmf_kernel), or int8 MFMAs on three
-// fixed-point planes of the activations (mm_kernel).  The first for bf16 and
-// f16 activations from 96 rows (measured, Q4_K / Q8_0 / Q6_K at 32 to 512
-// rows: 1.2-2.6x faster from 96 rows, slower below); f32 activations (three
-// bf16 planes, six MFMAs a product) are as fast or faster on the int8 planes.
+// The many-row product of float activations: the bf16 matrix cores
+// (mmf_kernel), or int8 MFMAs on three fixed-point planes of the activations
+// (mm_kernel).  The first for bf16 and f16 activations from the row counts
+// below, measured on Q8_0, Q4_0, Q4_K and Q6_K shapes at 17 to 512 rows: in
+// its dot mode (blocks of 32 without a minimum term) bf16 from 32 rows and
+// f16 from 64, otherwise from 96; f32 activations (three bf16 planes) are as
+// fast or faster on the int8 planes at every measured count.
 // KH_MANY_KERNEL ("float", "int8") forces one (a test hook read at each call).
-constexpr uint64_t MMF_ROWS = 96;
+bool mmf_dot_format(uint32_t fmt, uint32_t group) {
+    switch (fmt) {
+    case KH_Q8_0: case KH_Q4_0: case KH_Q5_0: case KH_IQ4_NL: return true;
+    case KH_INT8: case KH_INT4: return group == 32 || group == 64 || group == 128;
+    default: return false;
+    }
+}
 bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x_kind) {
     if (planes != 3 || !mm_group(fmt, group)) return false;
     const char *e = getenv("KH_MANY_KERNEL");
     if (e && !strcmp(e, "int8")) return false;
     if (e && !strcmp(e, "float")) return true;
-    return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= MMF_ROWS;
+    if (x_kind != KH_BF16 && x_kind != KH_F16) return false;
+    const uint64_t from = !mmf_dot_format(fmt, group) ? 96 : x_kind == KH_BF16 ? 32 : 64;
+    return rows >= from;
 }
 
 // The split of an mmf launch: column groups of the kernel's weight rows, row

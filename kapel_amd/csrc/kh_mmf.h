@@ -121,7 +121,9 @@ __device__ __forceinline__ void code_words(uint64_t c, uint32_t (&q)[2]) {
 constexpr int WAVES = 4;
 
 // The dot mode (codes as the B operand, one scale fma per output and group):
-// units of 128 elements without a minimum term.
+// units of 128 elements without a minimum term (Q8_0, Q4_0, Q5_0, IQ4_NL,
+// Kapel int8 / int4 in groups up to 128; the host's choice of kernel lists
+// the same formats, mmf_dot_format in kh_api.cpp).
 template <class F>
 constexpr bool dot_mode() { return !F::MIN && F::U == 128; }
 
