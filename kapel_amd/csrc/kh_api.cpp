@@ -288,11 +288,11 @@ DecodeKernel decode_kernel() {
 
 // The many-row product of float activations: the bf16 matrix cores
 // (mmf_kernel), or int8 MFMAs on three fixed-point planes of the activations
-// (mm_kernel).  The first for bf16 and f16 activations from the row counts
-// below, measured on Q8_0, Q4_0, Q4_K and Q6_K shapes at 17 to 512 rows: in
-// its dot mode (blocks of 32 without a minimum term) bf16 from 32 rows and
-// f16 from 64, otherwise from 96; f32 activations (three bf16 planes) are as
-// fast or faster on the int8 planes at every measured count.
+// (mm_kernel).  The first from the row counts below, measured on Q8_0, Q4_0,
+// Q4_K and Q6_K shapes at 17 to 512 rows: in its dot mode (blocks of 32
+// without a minimum term) bf16 from 32 rows, f16 and f32 from 64; otherwise
+// bf16 and f16 from 96, and f32 never (its three planes of split weights are
+// as fast or slower than the int8 planes at every measured count).
 // KH_MANY_KERNEL ("float", "int8") forces one (a test hook read at each call).
 bool mmf_dot_format(uint32_t fmt, uint32_t group) {
     switch (fmt) {
@@ -306,9 +306,8 @@ bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x
     const char *e = getenv("KH_MANY_KERNEL");
     if (e && !strcmp(e, "int8")) return false;
     if (e && !strcmp(e, "float")) return true;
-    if (x_kind != KH_BF16 && x_kind != KH_F16) return false;
-    const uint64_t from = !mmf_dot_format(fmt, group) ? 96 : x_kind == KH_BF16 ? 32 : 64;
-    return rows >= from;
+    if (!mmf_dot_format(fmt, group)) return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= 96;
+    return rows >= (x_kind == KH_BF16 ? 32u : 64u);
 }
 
 // The split of an mmf launch: column groups of the kernel's weight rows, row

@@ -148,13 +148,14 @@ struct Plan {
 };
 
 // Two workgroups a CU (two waves a SIMD, at most 256 registers each) for one
-// plane, and for two in the dot mode: one wave's waits for LDS, loads and
-// barriers are the other's MFMA time (measured: Q8_0 [gate; up] 24576 x 4096
-// at M = 512 with bf16 activations 415 us, against 479 us for one wave a SIMD
-// with 256 rows a workgroup).  One workgroup a CU otherwise (the registers
-// of three planes, or of two with split weights, would spill).
+// plane, and for every plane count in the dot mode: one wave's waits for LDS,
+// loads and barriers are the other's MFMA time (measured: Q8_0 [gate; up]
+// 24576 x 4096 at M = 512 with bf16 activations 415 us, against 479 us for one
+// wave a SIMD with 256 rows a workgroup; in f32, three planes, 534 us with 10
+// registers spilled against 667 us at one wave a SIMD).  One workgroup a CU
+// for split weights with two or three planes (their registers would spill).
 template <class F, int P>
-constexpr int occupancy_of() { return P == 1 || (P == 2 && dot_mode<F>()) ? 2 : 1; }
+constexpr int occupancy_of() { return P == 1 || dot_mode<F>() ? 2 : 1; }
 
 template <class F, int P, int WM, int WN>
 __global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs a) {
@@ -345,9 +346,11 @@ __global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs
             load_x(s + 3, X[(i + 1) & 1]);
             const int slot = i & 1;
             v4i xc[WM][P], xn[WM][P];
-            // Dot mode: the step's activations read at once (one wait).
-            v4i xall[DOT ? 4 : 1][WM][P];
-            if constexpr (DOT) {
+            // Dot mode with one plane: the step's activations read at once
+            // (one wait).
+            constexpr bool ALL = DOT && P == 1;
+            v4i xall[ALL ? 4 : 1][WM][P];
+            if constexpr (ALL) {
 #pragma unroll
                 for (int z = 0; z < 4; z++) read_x(slot, chunk(z), xall[z]);
                 asm volatile("" ::: "memory");
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs
 #pragma unroll
             for (int z = 0; z < 4; z++) {
                 const int jj = z / SPG, s2 = z % SPG, j = i * GS + jj;
-                if constexpr (DOT) {
+                if constexpr (ALL) {
 #pragma unroll
                     for (int mi = 0; mi < WM; mi++)
 #pragma unroll
@@ -398,7 +401,7 @@ __global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs
                                 for (int v = 0; v < 16; v++)
                                     acc[mi][t][v] = fmaf(dot[mi][t][v], sc[t][j], acc[mi][t][v]);
                 }
-                if (!DOT && z + 1 < 4)
+                if (!ALL && z + 1 < 4)
 #pragma unroll
                     for (int mi = 0; mi < WM; mi++)
 #pragma unroll
