@@ -135,9 +135,10 @@ def main():
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--configs", default="1,3,4,5,moe",
                     help="which of the other configs to run (comma-separated), after config 2")
-    ap.add_argument("--profile", choices=["gateup", "copy"],
+    ap.add_argument("--profile", choices=["gateup", "copy", "mmf4"],
                     help="only launch the [gate; up] call (or a 256 MiB device copy) "
-                         "20 times, for rocprofv3 counter runs")
+                         "20 times, or (mmf4) the four calls of config 4 with bf16 "
+                         "activations 10 times each, for rocprofv3 counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -183,6 +184,19 @@ def main():
             nbytes += data.size
         return host, nbytes
 
+    if args.profile == "mmf4":
+        # The four calls of the Q8_0 layer of config 4 at M = 512 with bf16
+        # activations (the float many-row kernel), 10 times each.
+        qhost, _ = quantized_layer(QWEN_LAYER, 300, lambda r: ka.Q8_0)
+        qlayer = {name: ka.QuantizedTensor(torch.from_numpy(data).to(dev), fmt, 0, n, k)
+                  for name, (fmt, data, n, k) in qhost.items()}
+        for ci, call in enumerate(QWEN_CALLS):
+            k = qhost[call[0]][3]
+            x = torch.from_numpy(synth.normal(7 + ci, 512 * k, 1.0).reshape(512, k)).to(dev, torch.bfloat16)
+            for _ in range(10):
+                hip.forward(op, [x] + [qlayer[c] for c in call])
+        torch.cuda.synchronize()
+        return
     host, layer_bytes = quantized_layer(LAYER, 100, lambda r: fmts[r[0]])
     L = args.layers
     if args.profile == "gateup":
