@@ -15,7 +15,24 @@ __global__ __launch_bounds__(256) void prep_bf16_kernel(PrepBf16Args a) {
     if (e >= a.rows * a.kpad) return;
     const uint64_t m = e / a.kpad, k0 = e % a.kpad;
     uint32_t pl[3][4] = {};
-    if (k0 < a.k) {
+    // x of any alignment: vector loads when it is 16-byte aligned (every row
+    // then is: k is a multiple of 32), element loads otherwise.
+    const bool vec = ((uintptr_t)a.x & 15u) == 0;
+    if (k0 < a.k && !vec) {
+        const uint64_t at = m * a.k + k0;
+        for (int i = 0; i < 8; i++) {
+            float r;
+            if (a.x_kind == KH_F32) r = static_cast<const float *>(a.x)[at + i];
+            else if (a.x_kind == KH_BF16) r = __uint_as_float((uint32_t)static_cast<const uint16_t *>(a.x)[at + i] << 16);
+            else r = lanes::f16(static_cast<const uint16_t *>(a.x)[at + i]);
+            for (int p = 0; p < a.planes; p++) {
+                const uint32_t b = to_bf16(r);
+                pl[p][i / 2] |= b << (16 * (i % 2));
+                const float v = __uint_as_float(b << 16);
+                r = isfinite(v) ? r - v : 0.0f;
+            }
+        }
+    } else if (k0 < a.k) {
         const uint64_t at = m * a.k + k0;
         if (a.x_kind == KH_BF16) {
             const uint4 v = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.x) + at);

@@ -801,6 +801,25 @@ def test_unaligned_and_extreme_activations(hip):
             assert np.all(got[1] == 0.0)
 
 
+def test_unaligned_activations_of_the_float_many_row_kernel(hip):
+    """bf16, f16 and f32 activations 2 or 4 bytes off a 16-byte boundary at 96
+    rows (the float many-row kernel's choice for Q8_0), within 1e-4 (1 + |e|)
+    of the f64 product of the activations as given (f32 outputs)."""
+    k, n, rows = 512, 140, 96
+    data, w = weight(ka.Q8_0, 0, n, k, 34, hip)
+    dense = ko.dequantize(ka.Q8_0, 0, data).reshape(n, k)
+    x32 = np.random.default_rng(8).uniform(-1, 1, size=(rows, k)).astype(np.float32)
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        base = torch.zeros(rows * k + 1, dtype=dtype, device="cuda:0")
+        xt = base[1:].view(rows, k)
+        xt.copy_(dev(x32, dtype))
+        assert xt.data_ptr() % 16 != 0
+        x = xt.float().cpu().numpy().astype(np.float64)
+        got = product_f32_out(hip, xt, [w]).astype(np.float64)
+        e64 = x @ dense.T
+        assert np.all(np.abs(got - e64) <= 1e-4 * (1 + np.abs(e64))), dtype
+
+
 def test_outputs_written_in_full_and_workspace_reused(hip):
     """kapel-cuda/src/lib.rs:70-74 (outputs poisoned before each op: a part
     left unwritten gives NaN): every kernel path writes its whole output.
