@@ -296,6 +296,16 @@ def test_reused_activations(hip):
             hip.with_byte_activations(False)
         assert np.array_equal(first.view(np.uint32), plain[0].view(np.uint32))
         assert np.array_equal(second.view(np.uint32), plain[1].view(np.uint32)), byte
+    # The float many-row kernel's bf16 planes, reused: bf16 activations,
+    # Q8_0 at 64 rows (its dot mode) and Q4_K at 128 (split weights).
+    for fmt, rows in ((ka.Q8_0, 64), (ka.Q4K, 128)):
+        parts = [weight(fmt, 0, 300, k, 92, hip), weight(fmt, 0, 200, k, 93, hip)]
+        xb = dev(x_uniform(rows, k, 8), torch.bfloat16)
+        plain = [hip.forward(ka.QuantizedMatmul(), [xb, w]).cpu() for _, w in parts]
+        first = hip.forward(ka.QuantizedMatmul(), [xb, parts[0][1]]).cpu()
+        second = hip.forward(ka.QuantizedMatmul(), [xb, parts[1][1]], reuse_activations=True).cpu()
+        assert torch.equal(first.view(torch.int16), plain[0].view(torch.int16))
+        assert torch.equal(second.view(torch.int16), plain[1].view(torch.int16)), fmt
 
 
 def test_byte_mode_falls_back_for_other_formats(hip):
