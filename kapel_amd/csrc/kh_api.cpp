@@ -585,7 +585,11 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
     // bf16 planes, once for all weights: bf16 rows as they are, f16 rows in
     // two planes, f32 rows in three.
     const int fplanes = x_kind == KH_BF16 ? 1 : x_kind == KH_F16 ? 2 : 3;
-    if (need_mmf && !reuse) {
+    // bf16 rows already are the one plane when K is a multiple of 64 (no
+    // padding) and x is 16-byte aligned: the kernel reads x itself.
+    const bool direct = x_kind == KH_BF16 && k % 64 == 0 && ((uintptr_t)x & 15u) == 0;
+    const uint8_t *fbase = direct ? static_cast<const uint8_t *>(x) : ws + l.fplanes_off;
+    if (need_mmf && !reuse && !direct) {
         PrepBf16Args p{};
         p.x_kind = x_kind;
         p.x = x;
@@ -729,7 +733,7 @@ hipError_t plan_and_launch(const kh_weight *weights, uint32_t count, uint64_t k,
             a.width = c.width;
             a.partials = reinterpret_cast<float *>(ws + l.partials_off);
             if (L.mmf) {
-                a.planes = reinterpret_cast<const int8_t *>(ws + l.fplanes_off) + r0 * fplanes * l.kpad * 2;
+                a.planes = reinterpret_cast<const int8_t *>(fbase) + r0 * fplanes * l.kpad * 2;
                 a.planes_bytes = (uint32_t)((uint64_t)L.rows * fplanes * l.kpad * 2);
                 a.kpad = l.kpad;
                 err = launch_mmf(w.format, w.group, fplanes, a, s, nullptr);
