@@ -289,8 +289,9 @@ DecodeKernel decode_kernel() {
 // The many-row product of float activations: the bf16 matrix cores
 // (mmf_kernel), or int8 MFMAs on three fixed-point planes of the activations
 // (mm_kernel).  The first from the row counts below, measured on Q8_0, Q4_0,
-// Q4_K and Q6_K shapes at 17 to 512 rows: in its dot mode (blocks of 32
-// without a minimum term) bf16 from 32 rows, f16 and f32 from 64; otherwise
+// Q4_K and Q6_K shapes at 5 to 512 rows: in its dot mode (blocks of 32
+// without a minimum term) bf16 at every many-row count (Q8_0 [gate; up]
+// 24576 x 4096 at 5 rows 46 us against 57), f16 and f32 from 64; otherwise
 // bf16 and f16 from 96, and f32 never (its three planes of split weights are
 // as fast or slower than the int8 planes at every measured count).
 // KH_MANY_KERNEL ("float", "int8") forces one (a test hook read at each call).
@@ -307,7 +308,7 @@ bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x
     if (e && !strcmp(e, "int8")) return false;
     if (e && !strcmp(e, "float")) return true;
     if (!mmf_dot_format(fmt, group)) return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= 96;
-    return rows >= (x_kind == KH_BF16 ? 32u : 64u);
+    return x_kind == KH_BF16 || rows >= 64;
 }
 
 // The split of an mmf launch: column groups of the kernel's weight rows, row
