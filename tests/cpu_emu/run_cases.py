@@ -331,6 +331,19 @@ def main(which):
     case_float_kinds(Q4_1, 0, 40, 160, 30, F32, kernel="float")
     case_float_kinds(INT4, 64, 40, 320, 25, BF16, kernel="float")
     case_float_kinds(IQ3_S, 0, 40, 512, 100, BF16)
+    case_float_kinds(Q8_0, 0, 50, 32, 20, BF16)      # one block of K
+    case_float_kinds(Q4_0, 0, 70, 96, 70, BF16)      # K % 64 != 0: planes prepared, a unit past K
+    k = 256
+    parts = [(Q8_0, 0, blocks(Q8_0, 0, n * k // 32, 70 + i), n) for i, n in enumerate((150, 40))]
+    xf = xs(20, k, 9)
+    xb = (xf.view(np.uint32) >> 16).astype(np.uint16)
+    xf = (xb.astype(np.uint32) << 16).view(np.float32)
+    arr = (W * 2)(*[W(f, g, d.ctypes.data, d.size, n) for f, g, d, n in parts])
+    ws = workspace(L.kh_qmatmul_workspace(arr, 2, k, 20, 0))
+    out = np.full((20, 190), np.nan, np.float32)
+    assert L.kh_qmatmul(arr, 2, k, BF16, xb.ctypes.data, 20, F32, out.ctypes.data, 0, ws.ctypes.data,
+                        ws.size, None) == 0
+    check_f32("stacked many rows, bf16 (float kernel)", out, ko.product_f64(parts, k, xf))
     case_float_kinds(Q4K, 0, 300, 1024, 40, F32, kernel="int8")
     case_float_kinds(Q8_0, 0, 20, 256, 5, F32, kernel="float")
     k = 512
