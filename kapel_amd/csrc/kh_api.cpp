@@ -292,8 +292,10 @@ DecodeKernel decode_kernel() {
 // Q4_K and Q6_K shapes at 5 to 512 rows: in its dot mode (blocks of 32
 // without a minimum term) bf16 at every many-row count (Q8_0 [gate; up]
 // 24576 x 4096 at 5 rows 46 us against 57), f16 and f32 from 64; otherwise
-// bf16 and f16 from 96, and f32 never (its three planes of split weights are
-// as fast or slower than the int8 planes at every measured count).
+// bf16 and f16 from 96 (Q6_K and Q3_K, groups of 16, from 64: Q6_K 3072 x
+// 8192 at 64 rows 49 us against 57, Q3_K 12288 x 4096 58 against 83), and f32
+// never (its three planes of split weights are as fast or slower than the
+// int8 planes at every measured count).
 // KH_MANY_KERNEL ("float", "int8") forces one (a test hook read at each call).
 bool mmf_dot_format(uint32_t fmt, uint32_t group) {
     switch (fmt) {
@@ -307,7 +309,8 @@ bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x
     const char *e = getenv("KH_MANY_KERNEL");
     if (e && !strcmp(e, "int8")) return false;
     if (e && !strcmp(e, "float")) return true;
-    if (!mmf_dot_format(fmt, group)) return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= 96;
+    if (!mmf_dot_format(fmt, group))
+        return (x_kind == KH_BF16 || x_kind == KH_F16) && rows >= (fmt == KH_Q6K || fmt == KH_Q3K ? 64u : 96u);
     return x_kind == KH_BF16 || rows >= 64;
 }
 
