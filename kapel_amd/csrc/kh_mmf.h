@@ -1,24 +1,27 @@
 // The product by quantized weights for many rows of float activations (f32,
-// bf16 or f16) on gfx950's bf16 matrix cores.
-//
-// Each weight is decoded in registers to its f32 value, scale * code -
-// minimum (the CPU decoders' value, kapel-cpu/src/quantized.rs:403-682), and
-// split into three bf16 parts w0 + w1 + w2: the top 16 bits of the f32, the
-// top 16 bits of what is left, and the rest rounded to bf16 (the weight to
-// 2^-24 of its size, as its f32).  The activations come as P bf16 planes x0 +
-// .. (prep_bf16_kernel), exactly: bf16 rows as they are (P = 1), f16 rows in
-// two planes, f32 rows in three.  Then
-//
-//     y[m, n] = sum_k x[m, k] w[n, k] ~= sum_k sum_{i + j <= 2} x_i w_j
-//
-// in f32 MFMAs (v_mfma_f32_32x32x16_bf16) over all of K (3, 5 or 6 MFMAs a
-// tile and 16 elements for P = 1, 2, 3; the terms left out are below 2^-24
-// of the product): the weights' scales and minimums are in their values, so
-// no work per scale group is left for the VALU.  This is the arithmetic of the
-// CPU's many-row path (rows decoded to f32, then an f32 product:
+// bf16 or f16) on gfx950's bf16 matrix cores: the arithmetic of the CPU's
+// many-row path (rows decoded to f32, then an f32 product:
 // kapel-cpu/src/matmul.rs:198-239), each product to about f32's precision.
-// (Two parts a side, 16 bits, fail the CPU's tolerance 1e-4 (1 + |y|) where
-// large terms cancel.)
+//
+// The activations come as P exact bf16 planes x0 + .. (prep_bf16_kernel):
+// bf16 rows as they are (P = 1; read in place when K is a multiple of 64 and
+// x is 16-byte aligned), f16 rows in two planes, f32 rows in three.  The
+// weights take one of two modes:
+//
+// - dot mode (blocks of 32 without a minimum term: Q8_0, Q4_0, Q5_0, IQ4_NL,
+//   Kapel int8 / int4 in groups up to 128): the codes (at most 8 significant
+//   bits) are exact bf16 B operands; each group's dot sum_k q x over the
+//   planes is an f32 MFMA result (v_mfma_f32_32x32x16_bf16), then
+//   acc += scale * dot, one fma per output and group;
+// - split mode (the others): each weight's f32 value, scale * code - minimum
+//   (the CPU decoders' value, kapel-cpu/src/quantized.rs:403-682), is split
+//   into three bf16 parts w0 + w1 + w2 (the top 16 bits of the f32, the top
+//   16 bits of what is left, the rest rounded to bf16: the f32 exactly), and
+//       y[m, n] = sum_k x[m, k] w[n, k] ~= sum_k sum_{i + j <= 2} x_i w_j
+//   in f32 MFMAs over all of K (3, 5 or 6 a tile and 16 elements for P = 1,
+//   2, 3; the terms left out are below 2^-24 of the product).  Two parts a
+//   side (16 bits) fail the CPU's tolerance 1e-4 (1 + |y|) where large terms
+//   cancel.
 //
 // A workgroup of four waves takes RM = 32 WM activation rows by 4 x 32 WN
 // weight rows; wave w the weight rows 32 WN w .. + 32 WN of the group, for
@@ -32,9 +35,10 @@
 // K runs in steps of 64 elements.  The activations of a step ([P][RM][64]
 // bf16, 16-byte chunks swizzled by row) are loaded into registers two steps
 // ahead by every wave, written into one of two LDS slots one step ahead, and
-// read by all four waves; a wave's weight rows are loaded (buffer loads of
-// the lane readers of kh_mm.h) one unit ahead.  Every wait is the
-// compiler's: no direct-to-LDS copies.  Sums run in an order fixed by the
+// read by all four waves.  A wave's weight rows of a unit are copied by
+// coalesced 16-byte loads into registers a unit ahead, then into the wave's
+// own LDS slot, where the lane readers of kh_mm.h read them.  Every wait is
+// the compiler's: no direct-to-LDS copies.  Sums run in an order fixed by the
 // shapes (K in order within a workgroup, then the K splits in order by
 // mm_reduce_kernel).
 #pragma once
@@ -315,9 +319,9 @@ __global__ __launch_bounds__(256, (occupancy_of<F, P>())) void mmf_kernel(MmArgs
         // B operand (exact in bf16); each group's dot of codes and
         // activations, sum_k q x (planes summed), is an f32 MFMA result, and
         // joins the sums as acc += scale * dot (one fma per output and group).
-        // Other formats (a minimum term, or 256-element units whose scales
-        // and dot sums would not fit the registers of two waves a SIMD): the
-        // weights' values in three bf16 parts (split).
+        // Other formats (a minimum term, or 256-element units, for which the
+        // dot mode spills registers even at one wave a SIMD): the weights'
+        // values in three bf16 parts (split).
         constexpr bool DOT = dot_mode<F>();
         constexpr int WPARTS = DOT ? 1 : 3;
         constexpr int SPG = NB / 8;  // slots (16 elements of K) a group
