@@ -147,22 +147,14 @@ struct MmSplit {
     int wm, wmg, cols, mtiles, ngroups, units, ups, ks;
 };
 
-MmSplit mm_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std::vector<uint32_t> &members,
-                 int planes) {
-    const kh_weight &w = weights[members[0]];
-    MmSplit m{};
-    mm_shape(planes, (int)rows, m.wm, m.wmg);
-    m.cols = mm_cols(w.format, w.group, planes, (int)rows);
-    m.mtiles = (int)div_up(rows, 32 * m.wm * m.wmg);
-    m.ngroups = 0;
-    for (uint32_t i : members) m.ngroups += (int)div_up(weights[i].n, m.cols);
-    const int unit = mm_unit(w.format, w.group);
+// The K split of a many-row launch of m.mtiles x m.ngroups workgroups: the
+// time of a split is rounds of 256 workgroups times units each; a split is
+// taken when it saves more than 15 % (its partial sums cost a pass of their
+// own), each range keeping at least 512 elements of K.
+void split_k_of(MmSplit &m, int unit, uint64_t k) {
     m.units = (int)div_up(k, unit);
-    // The time of a split: rounds of 256 workgroups times units each; a
-    // split is taken when it saves more than 15 % (its partial sums cost a
-    // pass of their own).
-    uint64_t base = (uint64_t)m.mtiles * m.ngroups;
-    int most = std::max(1, m.units / (int)div_up(512, unit));
+    const uint64_t base = (uint64_t)m.mtiles * m.ngroups;
+    const int most = std::max(1, m.units / (int)div_up(512, unit));
     auto cost = [&](int ks) { return div_up(base * ks, 256) * div_up(m.units, ks); };
     int ks = 1;
     uint64_t best = cost(1);
@@ -173,6 +165,18 @@ MmSplit mm_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std:
         }
     m.ups = (int)div_up(m.units, ks);
     m.ks = (int)div_up(m.units, m.ups);
+}
+
+MmSplit mm_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std::vector<uint32_t> &members,
+                 int planes) {
+    const kh_weight &w = weights[members[0]];
+    MmSplit m{};
+    mm_shape(planes, (int)rows, m.wm, m.wmg);
+    m.cols = mm_cols(w.format, w.group, planes, (int)rows);
+    m.mtiles = (int)div_up(rows, 32 * m.wm * m.wmg);
+    m.ngroups = 0;
+    for (uint32_t i : members) m.ngroups += (int)div_up(weights[i].n, m.cols);
+    split_k_of(m, mm_unit(w.format, w.group), k);
     return m;
 }
 
@@ -319,7 +323,7 @@ bool use_mmf(uint32_t fmt, uint32_t group, uint64_t rows, int planes, uint32_t x
 }
 
 // The split of an mmf launch: column groups of the kernel's weight rows, row
-// tiles of 128, K split as mm_split does.
+// tiles of 128 (the kernel recounts its own), K split as mm_split does.
 MmSplit mmf_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std::vector<uint32_t> &members) {
     const kh_weight &w = weights[members[0]];
     MmSplit m{};
@@ -327,20 +331,7 @@ MmSplit mmf_split(uint64_t rows, uint64_t k, const kh_weight *weights, const std
     m.mtiles = (int)div_up(rows, 128);
     m.ngroups = 0;
     for (uint32_t i : members) m.ngroups += (int)div_up(weights[i].n, m.cols);
-    const int unit = mm_unit(w.format, w.group);
-    m.units = (int)div_up(k, unit);
-    uint64_t base = (uint64_t)m.mtiles * m.ngroups;
-    int most = std::max(1, m.units / (int)div_up(512, unit));
-    auto cost = [&](int ks) { return div_up(base * ks, 256) * div_up(m.units, ks); };
-    int ks = 1;
-    uint64_t best = cost(1);
-    for (int s = 2; s <= most; s++)
-        if (cost(s) * 100 < best * 85) {
-            ks = s;
-            best = cost(s);
-        }
-    m.ups = (int)div_up(m.units, ks);
-    m.ks = (int)div_up(m.units, m.ups);
+    split_k_of(m, mm_unit(w.format, w.group), k);
     return m;
 }
 
