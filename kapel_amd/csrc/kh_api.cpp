@@ -229,10 +229,10 @@ Gemv2 gemv2_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
 
 // The streamed decode kernel (gemv4_kernel): for one row of f32 activations
 // or up to four of bytes.  `tiles` tiles a workgroup and `ks` waves a tile
-// (contiguous ranges of units of K), as many workgroups as take at least one
-// round of the CUs with eight multiplying waves a workgroup; each wave's ring
-// holds its whole stream when that fits, else a multiple of both a copy (64
-// chunks) and a unit.
+// (contiguous ranges of units of K).  One matrix (`single`): one wave a tile,
+// walking tiles; several: one tile of eight waves a workgroup.  Each wave's
+// ring holds its whole stream when that fits, else a multiple of both a copy
+// (64 chunks) and a unit.
 struct Gemv4 {
     bool ok = false;
     int tiles, ks, npw, tb;
@@ -241,7 +241,7 @@ struct Gemv4 {
 
 static int gcd_int(int a, int b) { return b ? gcd_int(b, a % b) : a; }
 
-Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, int tiles_total) {
+Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, int tiles_total, bool single) {
     Gemv4 p;
     const int unit = gemv_unit(fmt, group);
     const int len = (int)kh_block_len(fmt, group), bytes = (int)kh_block_bytes(fmt, group);
@@ -255,17 +255,54 @@ Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     // Preparing waves: one pass of loads over the activations where eight
     // waves take them (256 quads a wave).
     p.npw = std::max(1, std::min(8, (int)div_up(quads, 256)));
-    // One tile of eight waves a workgroup (two workgroups a CU).
+    const int step = 64 / gcd_int(64, uc) * uc / 64;  // copies of lcm(64, uc) chunks
+    const size_t span = (size_t)units * unit;
+    auto head_of = [&](int tiles, int waves) {
+        size_t h = 16 + (size_t)rows * planes * span + span + (size_t)rows * (span / 32) * 16 +
+                   (size_t)tiles * waves * 16 * rows * 4;
+        return (h + 15) / 16 * 16;
+    };
+    if (single) {
+        // One matrix: one wave a tile, each wave walking every gridDim-th
+        // tile after its first in one stream of copies (the workgroups that
+        // are resident at once).  The smallest ring of whole units that
+        // holds two units and a copy (one tile's stream when that is
+        // smaller and whole units), and the tiles a workgroup that give the
+        // fewest rounds of walking waves: launch time is the most tiles a
+        // wave walks times the time of a tile, which from eight walking
+        // waves a CU grows with the waves a CU (measured on the 151936 x
+        // 4096 Q6_K table: 8 or 10 walking waves a CU 141 us, 9 172 us, 6
+        // 198 us, one tile of eight waves a workgroup 161 us).
+        int tb = (2 * uc + 64 + step * 64 - 1) / (step * 64) * step;
+        const int one = (int)div_up((uint64_t)units * uc, 64);
+        if (one < tb && one * 64 % uc == 0) tb = one;
+        long best = 0, best_w = 0;
+        for (int T = 1; p.npw + T <= 16; T++) {
+            const size_t lds = head_of(T, 1) + (size_t)T * tb * 1024;
+            if (lds > limit) break;
+            const int per_cu = std::max(1, std::min((int)((160 * 1024) / lds), 32 / (p.npw + T)));
+            const long W = (long)per_cu * T;  // walking waves a CU
+            const long rounds = (long)div_up((uint64_t)tiles_total, (uint64_t)cu_count() * W);
+            const long score = rounds * std::max<long>(W, 8);
+            // Ties: fewer waves a CU, then more tiles a workgroup.
+            if (p.ok && (score > best || (score == best && W > best_w))) continue;
+            best = score;
+            best_w = W;
+            p.ok = true;
+            p.tiles = T;
+            p.ks = 1;
+            p.tb = tb;
+        }
+        return p;
+    }
+    // Several matrices: one tile of eight waves a workgroup (two workgroups
+    // a CU).
     const int T = 1;
     int ks = std::min(units, 8);
-    const int step = 64 / gcd_int(64, uc) * uc / 64;  // copies of lcm(64, uc) chunks
     for (; ks >= 1; ks--) {
         if (p.npw + T * ks > 16) continue;
         const int upw = (int)div_up(units, ks);
-        const size_t span = (size_t)units * unit;
-        size_t head = 16 + (size_t)rows * planes * span + span + (size_t)rows * (span / 32) * 16 +
-                      (size_t)T * ks * 16 * rows * 4;
-        head = (head + 15) / 16 * 16;
+        const size_t head = head_of(T, ks);
         if (head >= limit) return p;
         const int whole = (int)div_up((uint64_t)upw * uc, 64);
         int tb = (int)((limit - head) / ((size_t)T * ks * 1024));
@@ -464,7 +501,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
                 // staged), or where the caller asks for it.
                 const DecodeKernel dk = decode_kernel();
                 if (dk == DecodeKernel::STREAMED || (dk == DecodeKernel::AUTO && L.tiles >= 8 * cu_count()))
-                    L.g4 = gemv4_plan(w.format, w.group, k, L.rows, planes, L.tiles);
+                    L.g4 = gemv4_plan(w.format, w.group, k, L.rows, planes, L.tiles, L.members.size() == 1);
             }
             fn(L);
             continue;

@@ -828,11 +828,15 @@ hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
     if (a.dma == 4) {
         // Host-side checks of what the kernel assumes: its waves, a ring
         // that holds the whole stream or a multiple of a unit and a copy of
-        // at least two units.
+        // at least two units.  A wave that walks several tiles has a stream
+        // longer than one tile's: its ring must be whole units (a unit's
+        // chunks never wrap).
         constexpr int UC = 16 * Unit<F>::CW;
         const int upw = (a.units + a.kw - 1) / a.kw;
         const int whole = (upw * UC + 63) / 64;
-        const bool ring_ok = a.tb >= whole || ((a.tb * 64) % UC == 0 && a.tb * 64 >= 2 * UC + 64);
+        const bool walk = a.kw == 1 && a.count == 1;
+        const bool ring_ok = (a.tb * 64) % UC == 0 ? a.tb >= whole || a.tb * 64 >= 2 * UC + 64
+                                                    : !walk && a.tb >= whole;
         const size_t lds = gemv4_lds(a.rows, P, a.units, F::U, a.tiles, a.kw, a.tb);
         if (a.npw < 1 || a.tiles < 1 || a.kw < 1 || a.npw + a.tiles * a.kw > 16 || a.tb < 1 || !ring_ok ||
             lds > (size_t)(160 * 1024 - grid_lds<F>()) || mt > 1)

@@ -291,6 +291,14 @@ def main(which):
     case_product(Q6K, 0, 33, 1024, 3)
     case_product(Q4K, 0, 40, 4096, 1)       # decode: K split over 4 workgroups
     case_product(Q6K, 0, 48, 8192, 1)       # decode: K split over 8 workgroups
+    # The streamed decode kernel (launches of eight or more rounds of the
+    # emulator's two CUs): one wave a tile, each walking several tiles
+    # through a ring of whole units smaller than its stream.
+    case_product(Q6K, 0, 600, 1024, 1)
+    case_product(Q4K, 0, 520, 256, 1)       # one unit of K: a ring of four units
+    case_product(Q8_0, 0, 600, 1024, 1)     # units of 128
+    case_product(IQ3_S, 0, 300, 512, 1)     # the grid in LDS
+    case_bytes(Q4K, 0, 600, 1024, 3)
     case_product(Q4K, 0, 100, 2048, 8)      # K in two chunks of the small-M product
     case_product(Q4_0, 0, 40, 4096, 5)      # four chunks, two waves per tile
     case_product(Q3K, 0, 20, 2048, 7)
