@@ -147,6 +147,54 @@ def test_streamed_decode_of_every_format(hip, streamed, fmt, group):
         check_f32(got, ko.product_f64(parts, k, x), f"streamed stack fmt {fmt}/{group}")
 
 
+def fast_blocks(fmt, n, k, seed):
+    """Random codes with f16 scales in [0.005, 0.02) from numpy's generator:
+    the bytes of a large matrix in a fraction of a second."""
+    size, count = ko.block_bytes(fmt, 0), n * k // ko.block_len(fmt, 0)
+    rng = np.random.default_rng(seed)
+    raw = rng.integers(0, 256, (count, size), dtype=np.uint8)
+    for at in HALVES[fmt]:
+        h = rng.uniform(0.005, 0.02, count).astype(np.float16).view(np.uint16)
+        raw[:, at:at + 2] = h.view(np.uint8).reshape(count, 2)
+    return raw.ravel()
+
+
+def test_streamed_decode_walking_many_tiles(hip):
+    """Launches of eight and more rounds of the CUs take the streamed kernel
+    with one wave a tile, each wave walking several tiles through a ring of
+    whole units (a ring of one tile's units for Q6_K at K = 1024, of four
+    units over two-unit tiles for Q4_K at K = 512, units of 128 with the last
+    one past K for Q8_0 at K = 1312), the last tile ragged: every row against
+    f64, a bitwise rerun, and the staged kernel within the bar."""
+    for fmt, n, k in ((ka.Q4K, 65541, 512), (ka.Q6K, 40003, 1024), (ka.Q8_0, 33007, 1312)):
+        data = fast_blocks(fmt, n, k, 300 + fmt)
+        w = ka.QuantizedTensor(dev(data), fmt, 0, n, k)
+        x = x_uniform(1, k, 7 + fmt)
+        e64 = ko.product_f64([(fmt, 0, data, n)], k, x)
+        got = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        check_f32(got, e64, f"walking fmt {fmt} n {n} k {k}")
+        again = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+        os.environ["KH_DECODE_KERNEL"] = "staged"
+        try:
+            staged = hip.forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+        finally:
+            os.environ.pop("KH_DECODE_KERNEL", None)
+        assert np.all(np.abs(got - staged) <= 2e-4 * (1 + np.abs(e64)))
+    # Byte activations, three rows: the product of the quantized rows.
+    n, k = 40003, 512
+    data = fast_blocks(ka.Q4K, n, k, 333)
+    w = ka.QuantizedTensor(dev(data), ka.Q4K, 0, n, k)
+    x = byte_x(3, k)
+    q, s_, _ = ko.quantize_x(x)
+    xq = np.repeat(s_.astype(np.float64), 32, axis=1) * q.astype(np.float64)
+    dense = ko.dequantize(ka.Q4K, 0, data).reshape(n, k)
+    e, size = xq @ dense.T, np.abs(xq) @ np.abs(dense).T
+    got = hip.with_byte_activations(True).forward(ka.QuantizedMatmul(), [dev(x), w]).cpu().numpy()
+    hip.with_byte_activations(False)
+    assert np.all(np.abs(got - e) <= 1e-5 * size + 1e-6)
+
+
 def test_streamed_decode_with_byte_activations(hip, streamed):
     """The streamed kernel with byte activations (up to four rows) is the
     product of the quantized activations (bytes.rs:753-770)."""
