@@ -135,10 +135,11 @@ def main():
     ap.add_argument("--no-configs", action="store_true")
     ap.add_argument("--configs", default="1,3,4,5,moe",
                     help="which of the other configs to run (comma-separated), after config 2")
-    ap.add_argument("--profile", choices=["gateup", "copy", "mmf4"],
-                    help="only launch the [gate; up] call (or a 256 MiB device copy) "
-                         "20 times, or (mmf4) the four calls of config 4 with bf16 "
-                         "activations 10 times each, for rocprofv3 counter runs")
+    ap.add_argument("--profile", choices=["gateup", "copy", "mmf4", "table"],
+                    help="only launch the [gate; up] call (or a 256 MiB device copy, or "
+                         "(table) config 5's Q6_K output table at M = 1) 20 times, or "
+                         "(mmf4) the four calls of config 4 with bf16 activations 10 "
+                         "times each, for rocprofv3 counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -195,6 +196,17 @@ def main():
             x = torch.from_numpy(synth.normal(7 + ci, 512 * k, 1.0).reshape(512, k)).to(dev, torch.bfloat16)
             for _ in range(10):
                 hip.forward(op, [x] + [qlayer[c] for c in call])
+        torch.cuda.synchronize()
+        return
+    if args.profile == "table":
+        # Config 5's 151936 x 4096 Q6_K output table at M = 1 (the streamed
+        # decode kernel, walking), as the bench times it.
+        table = ka.quantize(ka.Q6K, 0, values(77, 151936 * 4096))
+        wt = ka.QuantizedTensor(torch.from_numpy(table).to(dev), ka.Q6K, 0, 151936, 4096)
+        xt = torch.from_numpy(synth.normal(6, 4096, 1.0).reshape(1, 4096)).to(dev)
+        ot = torch.empty((1, 151936), device=dev)
+        for _ in range(20):
+            hip.forward(op, [xt, wt], out=ot)
         torch.cuda.synchronize()
         return
     host, layer_bytes = quantized_layer(LAYER, 100, lambda r: fmts[r[0]])
