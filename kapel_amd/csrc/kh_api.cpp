@@ -241,7 +241,8 @@ struct Gemv4 {
 
 static int gcd_int(int a, int b) { return b ? gcd_int(b, a % b) : a; }
 
-Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, int tiles_total, bool single) {
+Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes, uint32_t x_kind, int tiles_total,
+                 bool single) {
     Gemv4 p;
     const int unit = gemv_unit(fmt, group);
     const int len = (int)kh_block_len(fmt, group), bytes = (int)kh_block_bytes(fmt, group);
@@ -265,28 +266,45 @@ Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
     if (single) {
         // One matrix: one wave a tile, each wave walking every gridDim-th
         // tile after its first in one stream of copies (the workgroups that
-        // are resident at once).  The smallest ring of whole units that
-        // holds two units and a copy (one tile's stream when that is
-        // smaller and whole units), and the tiles a workgroup that give the
-        // fewest rounds of walking waves: launch time is the most tiles a
-        // wave walks times the time of a tile, which from eight walking
-        // waves a CU grows with the waves a CU (measured on the 151936 x
-        // 4096 Q6_K table: 8 or 10 walking waves a CU 141 us, 9 172 us, 6
-        // 198 us, one tile of eight waves a workgroup 161 us).
-        int tb = (2 * uc + 64 + step * 64 - 1) / (step * 64) * step;
+        // are resident at once).  The ring: the fewest whole units, at least
+        // two, in whole copies (one tile's stream when that is smaller and
+        // whole units).  The tiles a workgroup: the fewest rounds of walking
+        // waves, then the most walking waves a CU (the runtime's count of
+        // the workgroups a CU holds: registers, waves and LDS).  Measured on
+        // the 151936 x 4096 Q6_K table (80 VGPRs, 24 waves a CU): 2-unit
+        // rings, 8 walking and 4 preparing waves a workgroup, two a CU
+        // (16 walking waves a CU, 3 rounds) 113 us; 14 walking waves a CU
+        // 132 us; 12 121-145 us; rings of 4 units with 8 walking waves a
+        // CU 141 us.
+        int tb = (2 * uc + step * 64 - 1) / (step * 64) * step;
         const int one = (int)div_up((uint64_t)units * uc, 64);
         if (one < tb && one * 64 % uc == 0) tb = one;
-        long best = 0, best_w = 0;
+        long best_rounds = 0, best_w = 0;
         for (int T = 1; p.npw + T <= 16; T++) {
             const size_t lds = head_of(T, 1) + (size_t)T * tb * 1024;
             if (lds > limit) break;
-            const int per_cu = std::max(1, std::min((int)((160 * 1024) / lds), 32 / (p.npw + T)));
+            GemvArgs q{};
+            int per_cu = 0;
+            q.count = 1;
+            q.k = (int)k;
+            q.units = units;
+            q.rows = rows;
+            q.rows_total = rows;
+            q.mchunks = 1;
+            q.total_tiles = tiles_total;
+            q.x_kind = x_kind;
+            q.dma = 4;
+            q.npw = p.npw;
+            q.tiles = T;
+            q.kw = 1;
+            q.tb = tb;
+            q.occupancy = &per_cu;
+            if (launch_gemv(fmt, group, planes, q, nullptr) != hipSuccess || per_cu < 1)
+                per_cu = std::max(1, std::min((int)((160 * 1024) / lds), 32 / (p.npw + T)));
             const long W = (long)per_cu * T;  // walking waves a CU
             const long rounds = (long)div_up((uint64_t)tiles_total, (uint64_t)cu_count() * W);
-            const long score = rounds * std::max<long>(W, 8);
-            // Ties: fewer waves a CU, then more tiles a workgroup.
-            if (p.ok && (score > best || (score == best && W > best_w))) continue;
-            best = score;
+            if (p.ok && (rounds > best_rounds || (rounds == best_rounds && W < best_w))) continue;
+            best_rounds = rounds;
             best_w = W;
             p.ok = true;
             p.tiles = T;
@@ -501,7 +519,7 @@ void each_launch(const kh_weight *weights, uint32_t count, uint64_t k, uint64_t 
                 // staged), or where the caller asks for it.
                 const DecodeKernel dk = decode_kernel();
                 if (dk == DecodeKernel::STREAMED || (dk == DecodeKernel::AUTO && L.tiles >= 8 * cu_count()))
-                    L.g4 = gemv4_plan(w.format, w.group, k, L.rows, planes, L.tiles, L.members.size() == 1);
+                    L.g4 = gemv4_plan(w.format, w.group, k, L.rows, planes, x_kind, L.tiles, L.members.size() == 1);
             }
             fn(L);
             continue;

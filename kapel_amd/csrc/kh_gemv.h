@@ -799,15 +799,24 @@ hipError_t launch4(const GemvArgs &a, hipStream_t s, size_t lds) {
     hipError_t e = set_lds_limit(once, reinterpret_cast<const void *>(&gemv4_kernel<F, P, MT, XK>),
                                  160 * 1024 - grid_lds<F>());
     if (e != hipSuccess) return e;
+    const int threads = 64 * (a.npw + a.tiles * a.kw);
+    // Workgroups a CU holds at once (registers, waves, LDS), from the runtime.
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&gemv4_kernel<F, P, MT, XK>),
+                                                     threads, lds) != hipSuccess)
+        per_cu = 0;
+    if (a.occupancy) {
+        *a.occupancy = per_cu;
+        return hipSuccess;
+    }
     int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
     if (a.kw == 1 && a.count == 1) {
         // Each wave walks its tiles: as many workgroups as are resident at once.
-        const int waves = a.npw + a.tiles;
-        const int per_cu = std::max(1, std::min((int)((160 * 1024) / std::max<size_t>(lds, 1)), 32 / waves));
+        if (per_cu < 1)
+            per_cu = std::max(1, std::min((int)((160 * 1024) / std::max<size_t>(lds, 1)), 32 / (a.npw + a.tiles)));
         groups = std::min(groups, cu_count() * per_cu);
     }
-    hipLaunchKernelGGL((gemv4_kernel<F, P, MT, XK>), dim3((unsigned)groups), dim3(64 * (a.npw + a.tiles * a.kw)),
-                       lds, s, a);
+    hipLaunchKernelGGL((gemv4_kernel<F, P, MT, XK>), dim3((unsigned)groups), dim3(threads), lds, s, a);
     return hipGetLastError();
 }
 
@@ -827,15 +836,15 @@ hipError_t launch_fx(const GemvArgs &a, hipStream_t s) {
     int mt = P == 3 ? a.rows : (a.rows + 3) / 4;
     if (a.dma == 4) {
         // Host-side checks of what the kernel assumes: its waves, a ring
-        // that holds the whole stream or a multiple of a unit and a copy of
-        // at least two units.  A wave that walks several tiles has a stream
-        // longer than one tile's: its ring must be whole units (a unit's
-        // chunks never wrap).
+        // that holds the whole stream or whole units (at least two: a copy
+        // never overwrites the unit being multiplied) in whole copies.  A
+        // wave that walks several tiles has a stream longer than one tile's:
+        // its ring must be whole units (a unit's chunks never wrap).
         constexpr int UC = 16 * Unit<F>::CW;
         const int upw = (a.units + a.kw - 1) / a.kw;
         const int whole = (upw * UC + 63) / 64;
         const bool walk = a.kw == 1 && a.count == 1;
-        const bool ring_ok = (a.tb * 64) % UC == 0 ? a.tb >= whole || a.tb * 64 >= 2 * UC + 64
+        const bool ring_ok = (a.tb * 64) % UC == 0 ? a.tb >= whole || a.tb * 64 >= 2 * UC
                                                     : !walk && a.tb >= whole;
         const size_t lds = gemv4_lds(a.rows, P, a.units, F::U, a.tiles, a.kw, a.tb);
         if (a.npw < 1 || a.tiles < 1 || a.kw < 1 || a.npw + a.tiles * a.kw > 16 || a.tb < 1 || !ring_ok ||

@@ -374,6 +374,10 @@ __global__ __launch_bounds__(1024) void gemv4_kernel(GemvArgs a) {
     int64_t row0 = (int64_t)(first - tile_base) * 16;
     for (int J = 0, j = 0; J < nunits; J++) {
         for (const int lim = allowed(J); issued < lim; issued++) issue(issued);
+        // The last copy of unit J may have been issued just now: every lane
+        // issues it before any lane reads unit J (one instruction for the
+        // wave on the device; lanes that run apart in a host emulation).
+        __builtin_amdgcn_wave_barrier();
         // Unit J's copies are the first ((J + 1) UC + 63) / 64.
         wait_vm_n(min(63, issued - ((J + 1) * UC + 63) / 64));
         if (J == 0) KH_T(3);

@@ -161,6 +161,10 @@ struct GemvArgs {
     // (its outputs then NaN): 2^24; negative (a test of the path only):
     // give up at once.
     int spin_limit;
+    // Non-NULL (the streamed kernel only): nothing is launched; the
+    // workgroups of this shape that a CU holds at once are written here (0
+    // when the runtime cannot tell).
+    int *occupancy;
 #ifdef KH_TRACE
     int *trace;
 #endif

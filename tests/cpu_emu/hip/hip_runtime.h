@@ -377,6 +377,14 @@ inline hipError_t hipFuncGetAttributes(hipFuncAttributes *at, const void *) {
     at->sharedSizeBytes = 0;
     return hipSuccess;
 }
+// Workgroups a CU holds: by LDS and by 32 waves a CU (registers are not
+// modelled).
+inline hipError_t hipOccupancyMaxActiveBlocksPerMultiprocessor(int *n, const void *, int threads, size_t lds) {
+    const int by_waves = 32 / ((threads + 63) / 64);
+    const int by_lds = lds ? (int)(emu::LDS_BYTES / lds) : by_waves;
+    *n = by_waves < by_lds ? by_waves : by_lds;
+    return hipSuccess;
+}
 inline hipError_t hipFuncSetAttribute(const void *, hipFuncAttribute, int bytes) {
     return bytes <= (int)emu::LDS_BYTES ? hipSuccess : hipErrorInvalidValue;
 }
