@@ -271,11 +271,11 @@ Gemv4 gemv4_plan(uint32_t fmt, uint32_t group, uint64_t k, int rows, int planes,
         // whole units).  The tiles a workgroup: the fewest rounds of walking
         // waves, then the most walking waves a CU (the runtime's count of
         // the workgroups a CU holds: registers, waves and LDS).  Measured on
-        // the 151936 x 4096 Q6_K table (80 VGPRs, 24 waves a CU): 2-unit
-        // rings, 8 walking and 4 preparing waves a workgroup, two a CU
-        // (16 walking waves a CU, 3 rounds) 113 us; 14 walking waves a CU
-        // 132 us; 12 121-145 us; rings of 4 units with 8 walking waves a
-        // CU 141 us.
+        // the 151936 x 4096 Q6_K table (80 VGPRs, 24 waves a CU): two-unit
+        // rings, 8 walking and 4 preparing waves a workgroup, two a CU (16
+        // walking waves a CU, 3 rounds) 113-117 us; 14 walking waves a CU
+        // 132 us; 12, 121-145 us; four-unit rings with 8 walking waves a CU
+        // 141 us.
         int tb = (2 * uc + step * 64 - 1) / (step * 64) * step;
         const int one = (int)div_up((uint64_t)units * uc, 64);
         if (one < tb && one * 64 % uc == 0) tb = one;
