@@ -800,9 +800,11 @@ hipError_t launch4(const GemvArgs &a, hipStream_t s, size_t lds) {
                                  160 * 1024 - grid_lds<F>());
     if (e != hipSuccess) return e;
     const int threads = 64 * (a.npw + a.tiles * a.kw);
+    const bool walk = a.kw == 1 && a.count == 1;
     // Workgroups a CU holds at once (registers, waves, LDS), from the runtime.
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&gemv4_kernel<F, P, MT, XK>),
+    if ((walk || a.occupancy) &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(&gemv4_kernel<F, P, MT, XK>),
                                                      threads, lds) != hipSuccess)
         per_cu = 0;
     if (a.occupancy) {
@@ -810,7 +812,7 @@ hipError_t launch4(const GemvArgs &a, hipStream_t s, size_t lds) {
         return hipSuccess;
     }
     int groups = (a.total_tiles + a.tiles - 1) / a.tiles;
-    if (a.kw == 1 && a.count == 1) {
+    if (walk) {
         // Each wave walks its tiles: as many workgroups as are resident at once.
         if (per_cu < 1)
             per_cu = std::max(1, std::min((int)((160 * 1024) / std::max<size_t>(lds, 1)), 32 / (a.npw + a.tiles)));
