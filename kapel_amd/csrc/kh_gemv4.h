@@ -5,8 +5,10 @@
 // waves by contiguous ranges of units of K, plus `npw` preparing waves.  A
 // multiplying wave streams its 16 row segments unit after unit into a ring of
 // LDS of its own with direct-to-LDS copies (16 bytes a lane, 1 KiB a copy;
-// per unit the rows' chunks [row][CW] one after the other, CW odd, so that
-// the 16 rows of a read fall on different banks), keeping up to 56 copies in
+// per unit the rows' chunks [row][CW] one after the other, CW the 16-byte
+// chunks of a row's unit: odd for most formats, so that the 16 rows of a
+// read fall on different banks; Q6_K's 14 and Q2_K's 6 leave two rows a
+// bank, under 1 % of the table's time), keeping up to 56 copies in
 // flight, and multiplies each unit as soon as its own copies have landed
 // (`s_waitcnt vmcnt(n)` with n its later copies): the copies of later units
 // are in flight meanwhile.  The preparing waves load and prepare the
