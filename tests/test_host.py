@@ -155,6 +155,17 @@ def test_workspace_grows_with_rows_and_covers_the_split():
             assert ka.lib().kh_qmatmul_workspace(empty, 1, 0, rows, flags) > 0
 
 
+def test_workspace_of_a_launch_of_many_rounds_without_a_device():
+    """A launch of many rounds of the CUs (the 151936 x 4096 Q6_K table)
+    plans the streamed decode kernel, whose plan asks the runtime for its
+    occupancy: with no device the query fails and the plan falls back to its
+    own count; sizing the workspace (which plans f32 and bf16 activations
+    alike) still succeeds, at one row and at three rows in bytes."""
+    arr = (ka._Weight * 1)(weight_struct(ka.Q6K, 0, 151936, 4096))
+    assert ka.lib().kh_qmatmul_workspace(arr, 1, 4096, 1, 0) > 0
+    assert ka.lib().kh_qmatmul_workspace(arr, 1, 4096, 3, ka.BYTE_ACTIVATIONS) > 0
+
+
 def test_infer_mirrors_the_reference():
     """QuantizedMatmul::infer (kapel-ops/src/matmul.rs:105-150) on host tensors."""
     op = ka.QuantizedMatmul()
